@@ -1,0 +1,237 @@
+"""Benchmark of the MI355X attention hot path (one JSON line on stdout).
+
+Headline (`value`): paged decode attention throughput in algorithmic HBM GB/s on
+the bench-shaped decode step (config 3: store_kvcache of the new token + paged
+GQA decode, Qwen3-0.6B heads 16/8, head_dim 128, block_size 256, batch 256,
+context U[100, 2048], 2048-page pool).  A step is one such pass with inputs
+resident in HBM; consecutive steps alternate between independent cache pools so
+the 256 MB Infinity Cache cannot serve them.  Alongside: prefill TFLOP/s
+(config 4 prefix-cached, Qwen3-8B heads 32/8; config 2 varlen), fp8-KV decode
+GB/s (config 5), the roofline of the dominant kernel (HIP events on the launch
+stream) and the PyTorch CPU baseline (gather + SDPA) on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-cpu] [--only decode|prefill|fp8]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "nano-vllm_amd"))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, TFLOP/s
+METRIC = "paged decode attn HBM GB/s (% of peak) + prefill TFLOP/s, 1×MI355X"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _pools(case, n):
+    """n independent (k_cache, v_cache) pools with identical contents."""
+    pools = [(case.k_cache, case.v_cache)]
+    for _ in range(n - 1):
+        pools.append((case.k_cache.clone(), case.v_cache.clone()))
+    return pools
+
+
+def bench_decode(case, steps, warmup, n_pools=2, with_store=True):
+    import torch
+    import nanovllm_amd as nva
+    pools = _pools(case, n_pools)
+    q = case.q.unsqueeze(1)
+
+    def store(i):
+        kc, vc = pools[i % n_pools]
+        nva.store_kvcache(case.k_new, case.v_new, kc, vc, case.slot_mapping, case.k_scale, case.v_scale)
+
+    def attend(i):
+        kc, vc = pools[i % n_pools]
+        return nva.flash_attn_with_kvcache(q, kc, vc, case.context_lens, case.block_tables, case.scale,
+                                           k_scale=case.k_scale, v_scale=case.v_scale)
+
+    for i in range(warmup):
+        if with_store:
+            store(i)
+        attend(i)
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record()
+        if with_store:
+            store(i)
+        ev[i][1].record()
+        attend(i)
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = ev[0][0].elapsed_time(ev[-1][2]) / steps
+    attn_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
+    store_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    B = case.batch
+    D = case.num_kv_heads * case.head_dim
+    store_bytes = 2 * B * D * 2 + 2 * B * D * case.k_cache.element_size() + 4 * B if with_store else 0
+    attn_bytes = case.kv_bytes()
+    return dict(step_ms=step_ms, attn_ms=attn_ms, store_ms=store_ms, wall_ms=wall * 1e3 / steps,
+                attn_bytes=attn_bytes, store_bytes=store_bytes,
+                step_gbs=(attn_bytes + store_bytes) / (step_ms * 1e-3) / 1e9,
+                attn_gbs=attn_bytes / (attn_ms * 1e-3) / 1e9)
+
+
+def bench_prefill(case, steps, warmup):
+    import torch
+    import nanovllm_amd as nva
+    nva.store_kvcache(case.k, case.v, case.k_cache, case.v_cache, case.slot_mapping)
+    if case.block_tables is None:
+        k, v = case.k, case.v
+    else:
+        k, v = case.k_cache, case.v_cache
+
+    def run():
+        return nva.flash_attn_varlen_func(case.q, k, v, case.max_seqlen_q, case.cu_seqlens_q, case.max_seqlen_k,
+                                          case.cu_seqlens_k, case.scale, True, case.block_tables)
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record()
+        run()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    flops = case.flops()
+    return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
+
+
+def cpu_baseline_decode(case_gpu, budget_s=20.0):
+    """Reference-semantics PyTorch CPU decode step on a bounded sample of config 3."""
+    import torch
+    sys.path.insert(0, str(ROOT))
+    from oracle import cpu_baseline as CB
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    case = case_gpu.to("cpu")
+    B = case.batch
+    # sample: the first n sequences, n chosen from a one-sequence probe so the
+    # timed work stays within the budget
+    t0 = time.perf_counter()
+    CB.decode(case.q[:8], case.k_cache, case.v_cache, case.context_lens[:8], case.block_tables[:8], case.scale)
+    per_seq = (time.perf_counter() - t0) / 8
+    n = max(8, min(B, int(budget_s / 3 / max(per_seq, 1e-6))))
+    reps = 3
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        CB.store_kvcache(case.k_new[:n], case.v_new[:n], case.k_cache, case.v_cache, case.slot_mapping[:n])
+        CB.decode(case.q[:n], case.k_cache, case.v_cache, case.context_lens[:n], case.block_tables[:n], case.scale)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    L = sum(case.lengths[:n])
+    D = case.num_kv_heads * case.head_dim
+    bytes_ = L * D * 2 * 2 + n * case.num_heads * case.head_dim * 2 * 2 + 4 * n
+    bytes_ += 4 * sum(math.ceil(x / case.block_size) for x in case.lengths[:n]) + 2 * n * D * 2 * 2
+    return dict(value=bytes_ / t / 1e9, unit="GB/s", cores=threads, kind="port",
+                sample=f"config-3 decode step (index_copy_ store + block-table gather + SDPA, bf16) "
+                       f"over the first {n} of {B} sequences, median of {reps}, {t:.2f} s each")
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=["decode", "prefill", "fp8"], default=None)
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: the attention path has no cross-GPU step here "
+              f"(--gpus {args.gpus} requested); run with --gpus 1", file=sys.stderr)
+        return 2
+    import torch
+    import nanovllm_amd as nva
+    from nanovllm_amd import workloads as W
+    nva._capi.load()
+    dev = torch.device("cuda:0")
+    steps, warmup = args.steps, args.warmup
+    out = {}
+
+    if args.only in (None, "decode"):
+        log("[bench] config 3: decode step (store + paged decode), B=256")
+        c3 = W.config3(dev)
+        d3 = bench_decode(c3, steps, warmup)
+        log(f"[bench] cfg3 step {d3['step_ms']*1e3:.1f} us, attention {d3['attn_ms']*1e3:.1f} us "
+            f"= {d3['attn_gbs']:.0f} GB/s, store {d3['store_ms']*1e3:.1f} us")
+        out["cfg3"] = d3
+        if not args.no_cpu:
+            log("[bench] CPU baseline (config 3 sample)")
+            out["cpu"] = cpu_baseline_decode(c3)
+            log(f"[bench] cpu {out['cpu']['value']:.2f} GB/s on {out['cpu']['cores']} threads")
+        del c3
+        torch.cuda.empty_cache()
+    if args.only in (None, "prefill"):
+        log("[bench] config 4: prefix-cached prefill (Qwen3-8B heads)")
+        c4 = W.config4(dev)
+        out["cfg4"] = bench_prefill(c4, max(10, steps // 2), warmup)
+        log(f"[bench] cfg4 {out['cfg4']['ms']*1e3:.1f} us = {out['cfg4']['tflops']:.0f} TFLOP/s")
+        del c4
+        log("[bench] config 2: varlen prefill")
+        c2 = W.config2(dev)
+        out["cfg2"] = bench_prefill(c2, max(10, steps // 2), warmup)
+        log(f"[bench] cfg2 {out['cfg2']['ms']*1e3:.1f} us = {out['cfg2']['tflops']:.0f} TFLOP/s")
+        del c2
+        torch.cuda.empty_cache()
+    if args.only in (None, "fp8"):
+        log("[bench] config 5: fp8 KV decode, B=64, ctx U[16k,32k]")
+        c5 = W.config5(dev)
+        out["cfg5"] = bench_decode(c5, max(10, steps // 2), warmup)
+        log(f"[bench] cfg5 attention {out['cfg5']['attn_ms']*1e3:.1f} us = {out['cfg5']['attn_gbs']:.0f} GB/s")
+        del c5
+        torch.cuda.empty_cache()
+
+    line = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic: seeded N(0,1) bf16 q/k/v, random page tables (no checkpoint)"}
+    if "cfg3" in out:
+        d3 = out["cfg3"]
+        line["value"] = round(d3["step_gbs"], 1)
+        line["ms_per_step"] = round(d3["step_ms"], 5)
+        line["config"] = {"workload": "config 3: decode step = store_kvcache(new token) + paged GQA decode",
+                          "batch": 256, "context": "U[100,2048]", "num_heads": 16, "num_kv_heads": 8,
+                          "head_dim": 128, "block_size": 256, "pool_pages": 2048, "cache_pools_rotated": 2}
+        line["roofline"] = {"kernel": "paged decode (paged_decode_kernel + decode_merge_kernel)",
+                            "bound": "hbm", "achieved": round(d3["attn_gbs"], 1), "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s", "frac": round(d3["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                            "bytes_per_launch": d3["attn_bytes"], "launch_us": round(d3["attn_ms"] * 1e3, 2)}
+        line["store_kvcache_us"] = round(d3["store_ms"] * 1e3, 2)
+    if "cpu" in out:
+        line["cpu_baseline"] = out["cpu"]
+    if "cfg4" in out or "cfg2" in out:
+        line["prefill"] = {k: {"tflops": round(out[k]["tflops"], 1), "ms": round(out[k]["ms"], 4),
+                               "gflop": round(out[k]["flops"] / 1e9, 2),
+                               "frac_bf16_peak": round(out[k]["tflops"] / BF16_PEAK_TFLOPS, 4)}
+                           for k in ("cfg4", "cfg2") if k in out}
+    if "cfg5" in out:
+        d5 = out["cfg5"]
+        line["fp8_decode"] = {"cfg5": {"gbs": round(d5["attn_gbs"], 1), "frac": round(d5["attn_gbs"] / HBM_PEAK_GBS, 4),
+                                       "attn_us": round(d5["attn_ms"] * 1e3, 2), "bytes": d5["attn_bytes"]}}
+    if "value" not in line:
+        k = next(iter(out))
+        line["value"] = None
+        line["config"] = {"workload": k}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

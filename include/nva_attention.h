@@ -1,0 +1,133 @@
+/*
+ * nva_attention.h -- C ABI of the MI355X (gfx950) attention hot path of nano-vllm.
+ *
+ * Three device operations replace the three native calls inside
+ * nanovllm/layers/attention.py (reference, read-only):
+ *   nva_store_kvcache  <- store_kvcache / store_kvcache_kernel   attention.py:10-39
+ *   nva_prefill        <- flash_attn_varlen_func(..., causal=True,
+ *                         block_table=None | block_tables)         attention.py:67-73
+ *   nva_decode         <- flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
+ *                         cache_seqlens, block_table, softmax_scale,
+ *                         causal=True)                             attention.py:74-77
+ *
+ * Conventions shared by every entry point
+ *   - Plain pointers to device memory, sizes and strides in ELEMENTS (not bytes).
+ *   - Queries, keys, values and outputs are bf16 (the model dtype, model_runner.py:33).
+ *   - Paged caches are (num_blocks, block_size, num_kv_heads, head_dim), contiguous:
+ *     one slot is num_kv_heads*head_dim elements (the layout model_runner.py:136-148
+ *     allocates and attention.py:37 asserts).  A cache may hold bf16 or OCP fp8 e4m3fn
+ *     (NVA_DTYPE_FP8_E4M3) with one fp32 scale per kv head: real = fp8 * scale[h].
+ *   - Index tensors (slot_mapping, cu_seqlens, cache_seqlens, block tables) are int32,
+ *     as the reference's producers build them (model_runner.py:151-249).
+ *   - `stream` is a hipStream_t; every launch is enqueued on it, nothing synchronises,
+ *     nothing reads device memory on the host and nothing allocates device memory, so
+ *     the calls can be captured into a HIP graph (model_runner.py:296-336).
+ *   - Return 0 on success, otherwise an NVA_ERR_* code with a message retrievable by
+ *     nva_last_error() (thread-local).  Argument checks run before any HIP call, so
+ *     they are testable on a machine without a GPU; a rejected call writes nothing.
+ */
+#ifndef NVA_ATTENTION_H
+#define NVA_ATTENTION_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NVA_OK 0
+#define NVA_ERR_INVALID_ARGUMENT 1 /* shape, stride, alignment or pointer is wrong */
+#define NVA_ERR_UNSUPPORTED 2      /* valid but not implemented (e.g. head_dim != 128) */
+#define NVA_ERR_HIP 3              /* the HIP runtime rejected a launch */
+#define NVA_ERR_WORKSPACE 4        /* workspace missing or smaller than required */
+
+#define NVA_DTYPE_BF16 0
+#define NVA_DTYPE_FP8_E4M3 1
+
+/* Library version (major*10000 + minor*100 + patch). */
+int nva_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* nva_last_error(void);
+
+/*
+ * Scatter new keys/values into the paged caches.
+ * Replaces store_kvcache(key, value, k_cache, v_cache, slot_mapping), attention.py:32-39,
+ * and its Triton kernel store_kvcache_kernel, attention.py:10-29:
+ *   k_cache.flat[slot*D : slot*D + D] = key[i]      (D = num_kv_heads * head_dim)
+ * key/value are (num_tokens, num_kv_heads, head_dim) with head stride head_dim and
+ * element stride 1 (the asserts at attention.py:35-36); their row strides are free
+ * (value is a strided view of the fused qkv projection, qwen3.py:89).
+ * A slot outside [0, num_slots) is skipped (the reference has no guard; CUDA-graph
+ * padding rows would otherwise write slot 0).  For a bf16 cache the copy is bit-exact.
+ * For an fp8 cache each element is stored as e4m3fn(float(x) / scale[h]) with
+ * round-to-nearest-even; a magnitude above 464 (one that rounds past 448), an
+ * infinity or a NaN becomes NaN (0x7f | sign), bit-identical to
+ * (x.float() / scale).to(torch.float8_e4m3fn).
+ */
+int nva_store_kvcache(const void* key, int64_t key_row_stride,
+                      const void* value, int64_t value_row_stride,
+                      void* k_cache, void* v_cache, int64_t num_slots,
+                      const int32_t* slot_mapping, int64_t num_tokens,
+                      int32_t num_kv_heads, int32_t head_dim, int32_t cache_dtype,
+                      const float* k_scale, const float* v_scale, void* stream);
+
+/*
+ * Varlen causal prefill.  Replaces flash_attn_varlen_func(q, k, v, max_seqlen_q,
+ * cu_seqlens_q, max_seqlen_k, cu_seqlens_k, softmax_scale, causal=True, block_table),
+ * attention.py:67-73.
+ * q: (total_q, num_heads, head_dim); out: same shape.
+ * block_table == NULL: k/v are packed (total_k, num_kv_heads, head_dim) rows addressed by
+ *   cu_seqlens_k (row strides k_row_stride / v_row_stride, head stride head_dim).
+ * block_table != NULL: k/v are the paged caches (prefix-cache case, attention.py:68-69);
+ *   key j of sequence s lives in block block_table[s*bt_row_stride + j/block_size].
+ * Causal masking is bottom-right aligned: query i of a sequence with Lq queries and Lk
+ * keys sees keys j <= i + (Lk - Lq).  A query row with no visible key yields zeros.
+ * max_seqlen_q bounds the launch grid (host value, graph-capture safe).
+ */
+int nva_prefill(const void* q, int64_t q_row_stride,
+                const void* k, int64_t k_row_stride,
+                const void* v, int64_t v_row_stride,
+                const int32_t* block_table, int64_t bt_row_stride,
+                int32_t max_blocks_per_seq, int32_t block_size, int64_t num_blocks,
+                const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                int32_t num_seqs, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                float softmax_scale,
+                void* out, int64_t out_row_stride, void* stream);
+
+/*
+ * Workspace bytes nva_decode needs for these launch parameters (0 if it needs none).
+ * Depends only on host-side sizes, never on device contents.
+ */
+int64_t nva_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                   int32_t head_dim, int32_t max_blocks_per_seq,
+                                   int32_t block_size, int32_t kv_dtype, int32_t num_splits);
+
+/*
+ * Paged GQA decode: one query token per sequence over cache_seqlens[b] cached keys.
+ * Replaces flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
+ * cache_seqlens=context_lens, block_table=block_tables, softmax_scale, causal=True),
+ * attention.py:75-77 (causal is a no-op for one query).
+ * q/out: (batch, num_heads, head_dim).  block_table: (batch, >= max_blocks_per_seq).
+ * num_splits: 0 picks a split-K count from the sizes; n > 0 requests about n splits per
+ * sequence (as flash-attn's num_splits).  The key range of a sequence is clamped to
+ * max_blocks_per_seq*block_size; a block id outside [0, num_blocks) makes its keys
+ * masked; a sequence with no key yields zeros.
+ * kv_dtype NVA_DTYPE_FP8_E4M3: caches are e4m3fn with per-kv-head scales k_scale/v_scale.
+ */
+int nva_decode(const void* q, int64_t q_row_stride,
+               const void* k_cache, const void* v_cache, int32_t kv_dtype,
+               const float* k_scale, const float* v_scale, int64_t num_blocks,
+               const int32_t* cache_seqlens, const int32_t* block_table,
+               int64_t bt_row_stride, int32_t max_blocks_per_seq, int32_t block_size,
+               int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+               float softmax_scale, int32_t num_splits,
+               void* out, int64_t out_row_stride,
+               void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NVA_ATTENTION_H */

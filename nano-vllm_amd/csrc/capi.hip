@@ -1,0 +1,254 @@
+// extern "C" entry points declared in include/nva_attention.h: argument
+// validation, launch planning and error reporting.  Validation never touches
+// the GPU, so a rejected call is safe (and testable) on a host without one.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "nva_attention.h"
+#include "nva_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return NVA_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(NVA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace
+
+extern "C" {
+
+int nva_version(void) { return 100; }
+
+const char* nva_last_error(void) { return g_last_error.c_str(); }
+
+int nva_store_kvcache(const void* key, int64_t key_row_stride, const void* value,
+                      int64_t value_row_stride, void* k_cache, void* v_cache, int64_t num_slots,
+                      const int32_t* slot_mapping, int64_t num_tokens, int32_t num_kv_heads,
+                      int32_t head_dim, int32_t cache_dtype, const float* k_scale,
+                      const float* v_scale, void* stream) {
+  if (num_tokens < 0) return fail(NVA_ERR_INVALID_ARGUMENT, "num_tokens must be >= 0 (got %lld)", (long long)num_tokens);
+  if (num_tokens > 0x7fffffffLL) return fail(NVA_ERR_UNSUPPORTED, "num_tokens above 2^31-1");
+  if (num_kv_heads <= 0 || head_dim <= 0)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "num_kv_heads and head_dim must be positive (got %d, %d)", num_kv_heads, head_dim);
+  if (cache_dtype != NVA_DTYPE_BF16 && cache_dtype != NVA_DTYPE_FP8_E4M3)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "unknown cache dtype %d", cache_dtype);
+  if (num_tokens == 0) return ok();
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  const int64_t D = static_cast<int64_t>(num_kv_heads) * head_dim;
+  if (key_row_stride < D || value_row_stride < D)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "key/value row strides (%lld, %lld) must be >= num_kv_heads*head_dim (%lld)",
+                (long long)key_row_stride, (long long)value_row_stride, (long long)D);
+  if (num_slots <= 0) return fail(NVA_ERR_INVALID_ARGUMENT, "num_slots must be positive");
+  if (D > (1 << 20)) return fail(NVA_ERR_UNSUPPORTED, "num_kv_heads*head_dim above 2^20");
+  if (!aligned(slot_mapping, 4)) return fail(NVA_ERR_INVALID_ARGUMENT, "slot_mapping must be 4-byte aligned");
+
+  nva::StoreParams p{};
+  p.key = key;
+  p.value = value;
+  p.k_cache = k_cache;
+  p.v_cache = v_cache;
+  p.slot_mapping = slot_mapping;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.key_row_stride = key_row_stride;
+  p.value_row_stride = value_row_stride;
+  p.num_slots = num_slots;
+  p.num_tokens = num_tokens;
+  p.row_elems = static_cast<int32_t>(D);
+  p.head_dim = head_dim;
+  p.cache_dtype = cache_dtype;
+
+  int vec = 2;
+  if (cache_dtype == NVA_DTYPE_FP8_E4M3) {
+    if (!k_scale || !v_scale) return fail(NVA_ERR_INVALID_ARGUMENT, "fp8 cache needs k_scale and v_scale");
+    if (head_dim % 8 != 0) return fail(NVA_ERR_UNSUPPORTED, "fp8 store needs head_dim %% 8 == 0");
+    if (!aligned(key, 16) || !aligned(value, 16) || (key_row_stride % 8) || (value_row_stride % 8))
+      return fail(NVA_ERR_UNSUPPORTED, "fp8 store needs 16-byte aligned key/value rows");
+    if (!aligned(k_cache, 8) || !aligned(v_cache, 8))
+      return fail(NVA_ERR_INVALID_ARGUMENT, "fp8 caches must be 8-byte aligned");
+    if (!aligned(k_scale, 4) || !aligned(v_scale, 4)) return fail(NVA_ERR_INVALID_ARGUMENT, "scales must be 4-byte aligned");
+  } else {
+    for (int cand : {16, 8, 4}) {
+      if ((D * 2) % cand == 0 && (key_row_stride * 2) % cand == 0 && (value_row_stride * 2) % cand == 0 &&
+          aligned(key, cand) && aligned(value, cand) && aligned(k_cache, cand) && aligned(v_cache, cand)) {
+        vec = cand;
+        break;
+      }
+    }
+    if (!aligned(key, 2) || !aligned(value, 2) || !aligned(k_cache, 2) || !aligned(v_cache, 2))
+      return fail(NVA_ERR_INVALID_ARGUMENT, "bf16 tensors must be 2-byte aligned");
+  }
+  return hip_status(nva::launch_store_kvcache(p, vec, static_cast<hipStream_t>(stream)), "store_kvcache launch");
+}
+
+int nva_prefill(const void* q, int64_t q_row_stride, const void* k, int64_t k_row_stride, const void* v,
+                int64_t v_row_stride, const int32_t* block_table, int64_t bt_row_stride,
+                int32_t max_blocks_per_seq, int32_t block_size, int64_t num_blocks,
+                const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads, int32_t num_kv_heads,
+                int32_t head_dim, float softmax_scale, void* out, int64_t out_row_stride, void* stream) {
+  (void)max_seqlen_k;
+  if (head_dim != 128) return fail(NVA_ERR_UNSUPPORTED, "head_dim %d not supported (128 only)", head_dim);
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "num_heads (%d) must be a positive multiple of num_kv_heads (%d)", num_heads, num_kv_heads);
+  if (num_heads > 65535) return fail(NVA_ERR_UNSUPPORTED, "num_heads above 65535");
+  if (num_seqs < 0 || max_seqlen_q < 0) return fail(NVA_ERR_INVALID_ARGUMENT, "num_seqs and max_seqlen_q must be >= 0");
+  if (num_seqs > 65535) return fail(NVA_ERR_UNSUPPORTED, "num_seqs above 65535");
+  if (num_seqs == 0 || max_seqlen_q == 0) return ok();
+  if (!q || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k) return fail(NVA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  const int64_t hd = static_cast<int64_t>(num_heads) * head_dim;
+  const int64_t kd = static_cast<int64_t>(num_kv_heads) * head_dim;
+  if (q_row_stride < hd || out_row_stride < hd)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "q/out row strides must be >= num_heads*head_dim");
+  if (k_row_stride < kd || v_row_stride < kd)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "k/v row strides must be >= num_kv_heads*head_dim");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16) || (q_row_stride % 8) ||
+      (k_row_stride % 8) || (v_row_stride % 8) || (out_row_stride % 8))
+    return fail(NVA_ERR_UNSUPPORTED, "q/k/v/out must be 16-byte aligned with row strides a multiple of 8 elements");
+  if (!(softmax_scale > 0.f)) return fail(NVA_ERR_INVALID_ARGUMENT, "softmax_scale must be positive");
+  if (block_table) {
+    if (block_size <= 0 || block_size % 64 != 0)
+      return fail(NVA_ERR_UNSUPPORTED, "paged prefill needs block_size a positive multiple of 64 (got %d)", block_size);
+    if (max_blocks_per_seq <= 0 || bt_row_stride < max_blocks_per_seq || num_blocks <= 0)
+      return fail(NVA_ERR_INVALID_ARGUMENT, "block table shape is inconsistent");
+    if (!aligned(block_table, 4)) return fail(NVA_ERR_INVALID_ARGUMENT, "block_table must be 4-byte aligned");
+  }
+  nva::PrefillParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.block_table = block_table;
+  p.cu_q = cu_seqlens_q;
+  p.cu_k = cu_seqlens_k;
+  p.out = static_cast<uint16_t*>(out);
+  p.q_row_stride = q_row_stride;
+  p.k_row_stride = k_row_stride;
+  p.v_row_stride = v_row_stride;
+  p.out_row_stride = out_row_stride;
+  p.bt_row_stride = bt_row_stride;
+  p.num_blocks = num_blocks;
+  p.max_blocks = max_blocks_per_seq;
+  p.block_size = block_size;
+  p.num_seqs = num_seqs;
+  p.num_heads = num_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.group = num_heads / num_kv_heads;
+  p.scale_log2 = softmax_scale * kLog2e;
+  return hip_status(nva::launch_prefill(p, max_seqlen_q, static_cast<hipStream_t>(stream)), "prefill launch");
+}
+
+int64_t nva_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                   int32_t max_blocks_per_seq, int32_t block_size, int32_t kv_dtype,
+                                   int32_t num_splits) {
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks_per_seq <= 0 || head_dim <= 0) return 0;
+  const nva::DecodePlan plan =
+      nva::plan_decode(batch, num_kv_heads, max_blocks_per_seq, block_size, kv_dtype, num_splits);
+  if (plan.num_splits <= 1) return 0;
+  const int64_t rows = static_cast<int64_t>(batch) * num_heads * plan.num_splits;
+  return rows * head_dim * 4 + rows * 2 * 4;
+}
+
+int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache, int32_t kv_dtype,
+               const float* k_scale, const float* v_scale, int64_t num_blocks, const int32_t* cache_seqlens,
+               const int32_t* block_table, int64_t bt_row_stride, int32_t max_blocks_per_seq, int32_t block_size,
+               int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
+               int32_t num_splits, void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+               void* stream) {
+  if (head_dim != 128) return fail(NVA_ERR_UNSUPPORTED, "head_dim %d not supported (128 only)", head_dim);
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "num_heads (%d) must be a positive multiple of num_kv_heads (%d)", num_heads, num_kv_heads);
+  if (num_heads / num_kv_heads > 16)
+    return fail(NVA_ERR_UNSUPPORTED, "GQA group %d above 16 not supported", num_heads / num_kv_heads);
+  if (num_kv_heads > 65535) return fail(NVA_ERR_UNSUPPORTED, "num_kv_heads above 65535");
+  if (kv_dtype != NVA_DTYPE_BF16 && kv_dtype != NVA_DTYPE_FP8_E4M3)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "unknown kv dtype %d", kv_dtype);
+  if (batch < 0) return fail(NVA_ERR_INVALID_ARGUMENT, "batch must be >= 0");
+  if (batch > 65535) return fail(NVA_ERR_UNSUPPORTED, "batch above 65535");
+  if (num_splits < 0) return fail(NVA_ERR_INVALID_ARGUMENT, "num_splits must be >= 0");
+  if (block_size <= 0 || block_size % 32 != 0)
+    return fail(NVA_ERR_UNSUPPORTED, "decode needs block_size a positive multiple of 32 (got %d)", block_size);
+  if (max_blocks_per_seq <= 0 || bt_row_stride < max_blocks_per_seq)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "block table width %d / row stride %lld inconsistent", max_blocks_per_seq,
+                (long long)bt_row_stride);
+  if (static_cast<int64_t>(max_blocks_per_seq) * block_size > 0x7fffffffLL)
+    return fail(NVA_ERR_UNSUPPORTED, "max_blocks_per_seq*block_size above 2^31-1");
+  if (num_blocks <= 0) return fail(NVA_ERR_INVALID_ARGUMENT, "num_blocks must be positive");
+  if (batch == 0) return ok();
+  if (!q || !k_cache || !v_cache || !cache_seqlens || !block_table || !out)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (kv_dtype == NVA_DTYPE_FP8_E4M3 && (!k_scale || !v_scale))
+    return fail(NVA_ERR_INVALID_ARGUMENT, "fp8 kv cache needs k_scale and v_scale");
+  const int64_t hd = static_cast<int64_t>(num_heads) * head_dim;
+  if (q_row_stride < hd || out_row_stride < hd)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "q/out row strides must be >= num_heads*head_dim");
+  if (!aligned(q, 16) || !aligned(out, 16) || (q_row_stride % 8) || (out_row_stride % 8))
+    return fail(NVA_ERR_UNSUPPORTED, "q/out must be 16-byte aligned with row strides a multiple of 8 elements");
+  if (!aligned(k_cache, 16) || !aligned(v_cache, 16)) return fail(NVA_ERR_INVALID_ARGUMENT, "caches must be 16-byte aligned");
+  if (!aligned(cache_seqlens, 4) || !aligned(block_table, 4))
+    return fail(NVA_ERR_INVALID_ARGUMENT, "index tensors must be 4-byte aligned");
+  if (!(softmax_scale > 0.f)) return fail(NVA_ERR_INVALID_ARGUMENT, "softmax_scale must be positive");
+
+  const nva::DecodePlan plan =
+      nva::plan_decode(batch, num_kv_heads, max_blocks_per_seq, block_size, kv_dtype, num_splits);
+  const int64_t need = nva_decode_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
+                                                  block_size, kv_dtype, num_splits);
+  if (need > 0) {
+    if (!workspace || workspace_bytes < need)
+      return fail(NVA_ERR_WORKSPACE, "decode needs a workspace of %lld bytes (got %lld)", (long long)need,
+                  (long long)(workspace ? workspace_bytes : 0));
+    if (!aligned(workspace, 16)) return fail(NVA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  }
+  nva::DecodeParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k_cache = k_cache;
+  p.v_cache = v_cache;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.seqlens = cache_seqlens;
+  p.block_table = block_table;
+  p.out = static_cast<uint16_t*>(out);
+  const int64_t rows = static_cast<int64_t>(batch) * num_heads * plan.num_splits;
+  p.ws_o = need > 0 ? static_cast<float*>(workspace) : nullptr;
+  p.ws_ml = need > 0 ? static_cast<float*>(workspace) + rows * head_dim : nullptr;
+  p.q_row_stride = q_row_stride;
+  p.out_row_stride = out_row_stride;
+  p.bt_row_stride = bt_row_stride;
+  p.num_blocks = num_blocks;
+  p.batch = batch;
+  p.max_blocks = max_blocks_per_seq;
+  p.block_size = block_size;
+  p.num_heads = num_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.group = num_heads / num_kv_heads;
+  p.keys_per_split = plan.pages_per_split * block_size;
+  p.num_splits = plan.num_splits;
+  p.scale_log2 = softmax_scale * kLog2e;
+  return hip_status(nva::launch_decode(p, kv_dtype, static_cast<hipStream_t>(stream)), "decode launch");
+}
+
+}  // extern "C"

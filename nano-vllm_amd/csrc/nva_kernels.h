@@ -1,0 +1,89 @@
+// Kernel parameter blocks and launchers (internal; the public surface is
+// include/nva_attention.h).  All sizes and strides are in elements.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nva {
+
+struct StoreParams {
+  const void* key;            // bf16 (T, nkv, d)
+  const void* value;          // bf16 (T, nkv, d)
+  void* k_cache;              // (num_slots, nkv*d) bf16 or fp8
+  void* v_cache;
+  const int32_t* slot_mapping;
+  const float* k_scale;       // [nkv], fp8 only
+  const float* v_scale;
+  int64_t key_row_stride;
+  int64_t value_row_stride;
+  int64_t num_slots;
+  int64_t num_tokens;
+  int32_t row_elems;          // nkv * d
+  int32_t head_dim;
+  int32_t cache_dtype;        // 0 bf16, 1 fp8 e4m3fn
+};
+
+struct DecodeParams {
+  const uint16_t* q;          // (B, nh, 128) bf16, head stride 128
+  const void* k_cache;        // (num_blocks, block_size, nkv, 128)
+  const void* v_cache;
+  const float* k_scale;       // [nkv] (fp8) or null
+  const float* v_scale;
+  const int32_t* seqlens;     // [B]
+  const int32_t* block_table; // [B, bt_row_stride]
+  uint16_t* out;              // (B, nh, 128) bf16
+  float* ws_o;                // [B, nh, num_splits, 128] partial numerators
+  float* ws_ml;               // [B, nh, num_splits, 2] partial (max, sum)
+  int64_t q_row_stride;
+  int64_t out_row_stride;
+  int64_t bt_row_stride;
+  int64_t num_blocks;
+  int32_t batch;
+  int32_t max_blocks;         // usable block-table width
+  int32_t block_size;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t group;              // num_heads / num_kv_heads
+  int32_t keys_per_split;     // multiple of block_size
+  int32_t num_splits;
+  float scale_log2;           // softmax_scale * log2(e)
+};
+
+struct PrefillParams {
+  const uint16_t* q;          // (Tq, nh, 128) bf16
+  const uint16_t* k;          // packed (Tk, nkv, 128) or cache (slots, nkv, 128)
+  const uint16_t* v;
+  const int32_t* block_table; // null => packed
+  const int32_t* cu_q;        // [S+1]
+  const int32_t* cu_k;        // [S+1]
+  uint16_t* out;              // (Tq, nh, 128)
+  int64_t q_row_stride;
+  int64_t k_row_stride;
+  int64_t v_row_stride;
+  int64_t out_row_stride;
+  int64_t bt_row_stride;
+  int64_t num_blocks;
+  int32_t max_blocks;
+  int32_t block_size;
+  int32_t num_seqs;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t group;
+  int32_t num_q_tiles;        // ceil(max_seqlen_q * group / rows per workgroup)
+  float scale_log2;
+};
+
+hipError_t launch_store_kvcache(const StoreParams& p, int vec_bytes, hipStream_t stream);
+hipError_t launch_decode(const DecodeParams& p, int kv_dtype, hipStream_t stream);
+hipError_t launch_prefill(const PrefillParams& p, int max_seqlen_q, hipStream_t stream);
+
+// Split-K plan shared by nva_decode and nva_decode_workspace_bytes.
+struct DecodePlan {
+  int32_t pages_per_split;
+  int32_t num_splits;
+};
+DecodePlan plan_decode(int32_t batch, int32_t num_kv_heads, int32_t max_blocks,
+                       int32_t block_size, int32_t kv_dtype, int32_t requested_splits);
+
+}  // namespace nva

@@ -1,0 +1,121 @@
+// Paged KV-cache scatter (replaces the Triton store_kvcache_kernel of
+// nanovllm/layers/attention.py:10-29).
+//
+// One workgroup per new token.  Its threads stream the token's key row and
+// value row (D = num_kv_heads * head_dim bf16 each) in 16-byte pieces and write
+// them to slot `slot_mapping[token]` of the paged caches.  Every lane issues
+// one coalesced vector load and one vector store per piece; offsets are 64-bit
+// (slot * D overflows int32 beyond 2^21 slots).
+#include "nva_common.h"
+#include "nva_kernels.h"
+
+namespace nva {
+
+// VB bytes per lane per access (16, 8, 4 or 2: chosen on the host from the
+// alignment of pointers and row strides).
+template <int VB>
+__global__ __launch_bounds__(256) void store_kvcache_bf16_kernel(StoreParams p) {
+  const int64_t t = blockIdx.x;
+  const int64_t slot = p.slot_mapping[t];
+  if (slot < 0 || slot >= p.num_slots) return;
+  const int row_bytes = p.row_elems * 2;
+  const int pieces = row_bytes / VB;
+  const char* ksrc = static_cast<const char*>(p.key) + t * p.key_row_stride * 2;
+  const char* vsrc = static_cast<const char*>(p.value) + t * p.value_row_stride * 2;
+  char* kdst = static_cast<char*>(p.k_cache) + slot * row_bytes;
+  char* vdst = static_cast<char*>(p.v_cache) + slot * row_bytes;
+  // threadIdx.y selects key (0) or value (1)
+  const char* src = threadIdx.y ? vsrc : ksrc;
+  char* dst = threadIdx.y ? vdst : kdst;
+  for (int c = threadIdx.x; c < pieces; c += blockDim.x) {
+    if constexpr (VB == 16) {
+      st16(dst + c * 16, ld16(src + c * 16));
+    } else if constexpr (VB == 8) {
+      *reinterpret_cast<u32x2*>(dst + c * 8) = ld8(src + c * 8);
+    } else if constexpr (VB == 4) {
+      *reinterpret_cast<uint32_t*>(dst + c * 4) = *reinterpret_cast<const uint32_t*>(src + c * 4);
+    } else {
+      *reinterpret_cast<uint16_t*>(dst + c * 2) = *reinterpret_cast<const uint16_t*>(src + c * 2);
+    }
+  }
+}
+
+// f32 -> OCP e4m3fn with round-to-nearest-even on the grid extended by 480
+// (the NaN code 0x7f): magnitudes above 464, the midpoint of 448 and 480, and
+// infinities and NaNs map to NaN (0x7f) with the input's sign bit; exactly 464
+// ties to even (448).
+//  - |x| < 2^-6 (the subnormal range): adding 2^14 rounds |x| to a multiple of
+//    2^-9, the subnormal step, and the low mantissa bits of the sum are the code.
+//  - otherwise: round the 23-bit mantissa to 3 bits (ties to even) and rebias
+//    the exponent from 127 to 7.
+__device__ __forceinline__ uint32_t f32_to_e4m3fn(float x) {
+  uint32_t bits = __builtin_bit_cast(uint32_t, x);
+  const uint32_t sign = (bits >> 24) & 0x80u;
+  bits &= 0x7fffffffu;
+  uint32_t code;
+  if (bits > 0x43e80000u) {  // > 464.0f, inf or NaN
+    code = 0x7fu;
+  } else if (bits < 0x3c800000u) {  // < 2^-6
+    const float y = __builtin_bit_cast(float, bits) + 16384.0f;
+    code = __builtin_bit_cast(uint32_t, y) - 0x46800000u;
+  } else {
+    const uint32_t odd = (bits >> 20) & 1u;
+    bits += 0x7ffffu + odd;
+    code = (bits >> 20) - (120u << 3);
+  }
+  return code | sign;
+}
+
+// bf16 rows -> fp8 cache rows, 8 elements (16 B in, 8 B out) per lane.
+__global__ __launch_bounds__(256) void store_kvcache_fp8_kernel(StoreParams p) {
+  const int64_t t = blockIdx.x;
+  const int64_t slot = p.slot_mapping[t];
+  if (slot < 0 || slot >= p.num_slots) return;
+  const int pieces = p.row_elems / 8;
+  const bool is_v = threadIdx.y != 0;
+  const char* src = static_cast<const char*>(is_v ? p.value : p.key) +
+                    t * (is_v ? p.value_row_stride : p.key_row_stride) * 2;
+  char* dst = static_cast<char*>(is_v ? p.v_cache : p.k_cache) + slot * p.row_elems;
+  const float* scale = is_v ? p.v_scale : p.k_scale;
+  for (int c = threadIdx.x; c < pieces; c += blockDim.x) {
+    const float s = scale[(c * 8) / p.head_dim];
+    const u32x4 w = ld16(src + c * 16);
+    uint32_t out[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t word = w[2 * h + (e >> 1)];
+        const uint32_t b16 = (e & 1) ? (word >> 16) : (word & 0xffffu);
+        const float v = bf16_bits_to_f32(b16) / s;
+        packed |= f32_to_e4m3fn(v) << (8 * e);
+      }
+      out[h] = packed;
+    }
+    u32x2 o = {out[0], out[1]};
+    *reinterpret_cast<u32x2*>(dst + c * 8) = o;
+  }
+}
+
+hipError_t launch_store_kvcache(const StoreParams& p, int vec_bytes, hipStream_t stream) {
+  if (p.num_tokens == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(p.num_tokens));
+  if (p.cache_dtype == 1) {
+    const int pieces = p.row_elems / 8;
+    const dim3 block(pieces < 128 ? pieces : 128, 2);
+    hipLaunchKernelGGL(store_kvcache_fp8_kernel, grid, block, 0, stream, p);
+    return hipGetLastError();
+  }
+  const int pieces = p.row_elems * 2 / vec_bytes;
+  const dim3 block(pieces < 128 ? pieces : 128, 2);
+  switch (vec_bytes) {
+    case 16: hipLaunchKernelGGL(store_kvcache_bf16_kernel<16>, grid, block, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL(store_kvcache_bf16_kernel<8>, grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL(store_kvcache_bf16_kernel<4>, grid, block, 0, stream, p); break;
+    default: hipLaunchKernelGGL(store_kvcache_bf16_kernel<2>, grid, block, 0, stream, p); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace nva

@@ -1,0 +1,20 @@
+"""nano-vllm's attention hot path, MI355X-native (gfx950 HIP kernels behind a C ABI).
+
+Public surface, mirroring the reference package layout:
+  nanovllm_amd.layers.attention   Attention, store_kvcache, flash_attn_varlen_func,
+                                  flash_attn_with_kvcache
+  nanovllm_amd.utils.context      Context, get_context, set_context, reset_context
+"""
+from . import _capi
+from .layers.attention import (Attention, flash_attn_varlen_func, flash_attn_with_kvcache,
+                               store_kvcache)
+from .utils.context import Context, get_context, reset_context, set_context
+
+__all__ = [
+    "Attention", "store_kvcache", "flash_attn_varlen_func", "flash_attn_with_kvcache",
+    "Context", "get_context", "set_context", "reset_context", "library_path",
+]
+
+
+def library_path() -> str:
+    return str(_capi.LIB_PATH)

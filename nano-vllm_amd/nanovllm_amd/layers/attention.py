@@ -1,0 +1,217 @@
+"""Attention hot path on MI355X, mirroring nanovllm/layers/attention.py:1-79.
+
+The module keeps the reference's interface verbatim:
+  * store_kvcache(key, value, k_cache, v_cache, slot_mapping)   attention.py:32-39
+  * Attention(num_heads, head_dim, scale, num_kv_heads) with rebindable
+    k_cache / v_cache attributes and forward(q, k, v) -> o     attention.py:42-79
+and replaces the two flash-attn entry points it calls with functions of the same
+names and argument meaning, backed by the gfx950 HIP library through its C ABI:
+  * flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q, max_seqlen_k,
+    cu_seqlens_k, softmax_scale, causal=True, block_table=None)   attention.py:70-73
+  * flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens, block_table,
+    softmax_scale, causal=True)                                   attention.py:75-77
+
+Extension (not in the reference): an fp8 e4m3fn KV cache.  A module whose
+k_cache/v_cache are torch.float8_e4m3fn tensors must also carry k_scale/v_scale
+(float32, one per kv head); store_kvcache then quantises x / scale and decode
+dequantises on the fly.
+
+Every launch goes to torch's current stream, nothing synchronises and the only
+allocations are torch tensors (output, decode workspace), so decode can be
+captured in a CUDA/HIP graph as model_runner.py:296-336 does.  There is no
+fallback path: if the library is missing, calls raise.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .. import _capi
+from ..utils.context import get_context
+
+_BF16 = torch.bfloat16
+_FP8 = torch.float8_e4m3fn
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _cache_dtype_code(cache: torch.Tensor) -> int:
+    if cache.dtype == _BF16:
+        return _capi.NVA_DTYPE_BF16
+    if cache.dtype in (_FP8, torch.uint8):
+        return _capi.NVA_DTYPE_FP8_E4M3
+    raise RuntimeError(f"unsupported KV cache dtype {cache.dtype} (bfloat16 or float8_e4m3fn)")
+
+
+def _check_scales(code: int, k_scale, v_scale, num_kv_heads: int, device) -> None:
+    if code != _capi.NVA_DTYPE_FP8_E4M3:
+        return
+    for name, s in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if s is None:
+            raise RuntimeError(f"fp8 KV cache needs {name}")
+        if s.dtype != torch.float32 or s.numel() != num_kv_heads or not s.is_contiguous() or s.device != device:
+            raise RuntimeError(f"{name} must be a contiguous float32 tensor of {num_kv_heads} values on {device}")
+
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  slot_mapping: torch.Tensor, k_scale: torch.Tensor | None = None,
+                  v_scale: torch.Tensor | None = None):
+    """Scatter key/value rows into the paged caches (attention.py:32-39).
+
+    Same preconditions as the reference, raised as AssertionError like its asserts
+    (attention.py:35-38).  Slots outside [0, num_blocks*block_size) are skipped.
+    """
+    N, num_heads, head_dim = key.shape
+    D = num_heads * head_dim
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.stride(1) == D and v_cache.stride(1) == D
+    assert slot_mapping.numel() == N
+    if key.dtype != _BF16 or value.dtype != _BF16:
+        raise RuntimeError("key/value must be bfloat16")
+    if slot_mapping.dtype != torch.int32 or (N and not slot_mapping.is_contiguous()):
+        raise RuntimeError("slot_mapping must be a contiguous int32 tensor")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()) or k_cache.shape != v_cache.shape:
+        raise RuntimeError("k_cache/v_cache must be contiguous and of the same shape")
+    code = _cache_dtype_code(k_cache)
+    if _cache_dtype_code(v_cache) != code:
+        raise RuntimeError("k_cache and v_cache must share a dtype")
+    _check_scales(code, k_scale, v_scale, num_heads, k_cache.device)
+    num_slots = k_cache.numel() // D
+    lib = _capi.load()
+    _capi.check(lib.nva_store_kvcache(
+        key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+        k_cache.data_ptr(), v_cache.data_ptr(), num_slots,
+        slot_mapping.data_ptr(), N, num_heads, head_dim, code,
+        _ptr(k_scale), _ptr(v_scale), _stream(key)))
+
+
+def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, max_seqlen_q: int,
+                           cu_seqlens_q: torch.Tensor, max_seqlen_k: int, cu_seqlens_k: torch.Tensor,
+                           softmax_scale: float | None = None, causal: bool = True,
+                           block_table: torch.Tensor | None = None) -> torch.Tensor:
+    """Varlen causal attention over packed K/V, or over the paged caches when
+    block_table is given (attention.py:67-73).  q (total_q, nh, d) -> (total_q, nh, d)."""
+    if not causal:
+        raise RuntimeError("only causal=True is implemented (the only mode attention.py uses)")
+    total_q, nh, d = q.shape
+    if q.dtype != _BF16 or k.dtype != _BF16 or v.dtype != _BF16:
+        raise RuntimeError("q/k/v must be bfloat16 (an fp8 cache is read by decode only)")
+    if softmax_scale is None:
+        softmax_scale = d ** -0.5
+    if q.stride(-1) != 1 or q.stride(1) != d:
+        raise RuntimeError("q must have head stride head_dim and unit element stride")
+    for t in (cu_seqlens_q, cu_seqlens_k):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise RuntimeError("cu_seqlens must be contiguous int32 tensors")
+    num_seqs = cu_seqlens_q.numel() - 1
+    if cu_seqlens_k.numel() != num_seqs + 1:
+        raise RuntimeError("cu_seqlens_q and cu_seqlens_k must have the same length")
+    out = torch.empty((total_q, nh, d), dtype=_BF16, device=q.device)
+    if block_table is not None:
+        if k.dim() != 4 or not k.is_contiguous() or not v.is_contiguous() or k.shape != v.shape:
+            raise RuntimeError("paged k/v must be contiguous (num_blocks, block_size, nkv, d) caches")
+        num_blocks, block_size, nkv, _ = k.shape
+        if block_table.dtype != torch.int32 or block_table.stride(-1) != 1:
+            raise RuntimeError("block_table must be int32 with unit column stride")
+        k_row = v_row = nkv * d
+        bt_ptr, bt_stride, max_blocks = block_table.data_ptr(), block_table.stride(0), block_table.shape[1]
+    else:
+        if k.dim() != 3 or k.stride(-1) != 1 or v.stride(-1) != 1 or k.stride(1) != d or v.stride(1) != d:
+            raise RuntimeError("packed k/v must be (total_k, nkv, d) with head stride d")
+        nkv = k.shape[1]
+        k_row, v_row = k.stride(0), v.stride(0)
+        bt_ptr, bt_stride, max_blocks, block_size, num_blocks = None, 0, 0, 0, 0
+    lib = _capi.load()
+    _capi.check(lib.nva_prefill(
+        q.data_ptr(), q.stride(0), k.data_ptr(), k_row, v.data_ptr(), v_row,
+        bt_ptr, bt_stride, max_blocks, block_size, num_blocks,
+        cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), num_seqs, int(max_seqlen_q), int(max_seqlen_k),
+        nh, nkv, d, float(softmax_scale), out.data_ptr(), out.stride(0), _stream(q)))
+    return out
+
+
+def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                            cache_seqlens: torch.Tensor, block_table: torch.Tensor,
+                            softmax_scale: float | None = None, causal: bool = True, num_splits: int = 0,
+                            k_scale: torch.Tensor | None = None,
+                            v_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """Paged decode, one query per sequence (attention.py:75-77).
+    q (B, 1, nh, d) -> (B, 1, nh, d).  `causal` is accepted for signature parity
+    and is a no-op for a single query; num_splits has flash-attn's meaning
+    (0 = heuristic)."""
+    del causal
+    if q.dim() != 4 or q.shape[1] != 1:
+        raise RuntimeError("q must be (batch, 1, num_heads, head_dim)")
+    B, _, nh, d = q.shape
+    if q.dtype != _BF16:
+        raise RuntimeError("q must be bfloat16")
+    if q.stride(-1) != 1 or q.stride(2) != d:
+        raise RuntimeError("q must have head stride head_dim and unit element stride")
+    if softmax_scale is None:
+        softmax_scale = d ** -0.5
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise RuntimeError("caches must be contiguous (num_blocks, block_size, nkv, d) of one shape")
+    num_blocks, block_size, nkv, _ = k_cache.shape
+    code = _cache_dtype_code(k_cache)
+    if _cache_dtype_code(v_cache) != code:
+        raise RuntimeError("k_cache and v_cache must share a dtype")
+    _check_scales(code, k_scale, v_scale, nkv, k_cache.device)
+    if cache_seqlens.dtype != torch.int32 or not cache_seqlens.is_contiguous() or cache_seqlens.numel() != B:
+        raise RuntimeError("cache_seqlens must be a contiguous int32 tensor of batch size")
+    if block_table.dtype != torch.int32 or block_table.stride(-1) != 1 or block_table.shape[0] != B:
+        raise RuntimeError("block_table must be int32 (batch, max_blocks) with unit column stride")
+    max_blocks = block_table.shape[1]
+    out = torch.empty((B, 1, nh, d), dtype=_BF16, device=q.device)
+    lib = _capi.load()
+    ws_bytes = lib.nva_decode_workspace_bytes(B, nh, nkv, d, max_blocks, block_size, code, int(num_splits))
+    ws = torch.empty(max(ws_bytes, 0), dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
+    _capi.check(lib.nva_decode(
+        q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), code,
+        _ptr(k_scale), _ptr(v_scale), num_blocks,
+        cache_seqlens.data_ptr(), block_table.data_ptr(), block_table.stride(0), max_blocks, block_size,
+        B, nh, nkv, d, float(softmax_scale), int(num_splits),
+        out.data_ptr(), out.stride(0), _ptr(ws), ws_bytes, _stream(q)))
+    return out
+
+
+class Attention(nn.Module):
+    """Drop-in for nanovllm.layers.attention.Attention (attention.py:42-79)."""
+
+    def __init__(self, num_heads, head_dim, scale, num_kv_heads):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_kv_heads = num_kv_heads
+        self.k_cache = self.v_cache = torch.tensor([])
+        # fp8 cache extension: per-kv-head float32 scales, None for a bf16 cache
+        self.k_scale = self.v_scale = None
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+        q = q.view(-1, self.num_heads, self.head_dim)
+        k = k.view(-1, self.num_kv_heads, self.head_dim)
+        v = v.view(-1, self.num_kv_heads, self.head_dim)
+        context = get_context()
+        k_cache, v_cache = self.k_cache, self.v_cache
+        if k_cache.numel() and v_cache.numel():
+            store_kvcache(k, v, k_cache, v_cache, context.slot_mapping, self.k_scale, self.v_scale)
+        if context.is_prefill:
+            if context.block_tables is not None:  # prefix cache
+                k, v = k_cache, v_cache
+            o = flash_attn_varlen_func(q, k, v,
+                                       max_seqlen_q=context.max_seqlen_q, cu_seqlens_q=context.cu_seqlens_q,
+                                       max_seqlen_k=context.max_seqlen_k, cu_seqlens_k=context.cu_seqlens_k,
+                                       softmax_scale=self.scale, causal=True, block_table=context.block_tables)
+        else:  # decode
+            o = flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
+                                        cache_seqlens=context.context_lens, block_table=context.block_tables,
+                                        softmax_scale=self.scale, causal=True,
+                                        k_scale=self.k_scale, v_scale=self.v_scale)
+        return o.view(-1, self.num_heads * self.head_dim)

@@ -1,0 +1,42 @@
+"""Per-process attention metadata, mirroring nanovllm/utils/context.py:1-27.
+
+Same dataclass fields in the same order, the same module-global instance and
+the same get/set/reset functions, so producers written for the reference
+(model_runner.py:206-215, 243-248, 314-319) work unchanged.  Like the
+reference it is not thread-safe: one context per process, replaced wholesale
+by every set_context call.
+"""
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass
+class Context:
+    is_prefill: bool = False
+    cu_seqlens_q: torch.Tensor | None = None
+    cu_seqlens_k: torch.Tensor | None = None
+    max_seqlen_q: int = 0
+    max_seqlen_k: int = 0
+    slot_mapping: torch.Tensor | None = None
+    context_lens: torch.Tensor | None = None
+    block_tables: torch.Tensor | None = None
+
+
+_CONTEXT = Context()
+
+
+def get_context() -> Context:
+    return _CONTEXT
+
+
+def set_context(is_prefill, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=0, max_seqlen_k=0,
+                slot_mapping=None, context_lens=None, block_tables=None):
+    global _CONTEXT
+    _CONTEXT = Context(is_prefill, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                       slot_mapping, context_lens, block_tables)
+
+
+def reset_context():
+    global _CONTEXT
+    _CONTEXT = Context()

@@ -1,0 +1,163 @@
+"""The C ABI without a GPU: the library loads, exports every symbol that
+include/nva_attention.h declares, and rejects bad arguments with the documented
+error codes before any HIP call (so rejected calls are safe on a CPU host)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from nanovllm_amd import _capi
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "nva_attention.h"
+
+# fake, suitably aligned device addresses: validation rejects before dereferencing
+A = 0x10000
+B = 0x20000
+C = 0x30000
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _capi.load()
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(nva_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_lists_entry_points():
+    names = declared_functions()
+    assert {"nva_store_kvcache", "nva_prefill", "nva_decode", "nva_decode_workspace_bytes",
+            "nva_last_error", "nva_version"} <= set(names)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in {HEADER.name} but not exported"
+    assert set(declared_functions()) <= set(_capi.SIGNATURES)
+
+
+def test_version(lib):
+    assert lib.nva_version() >= 100
+
+
+def store(lib, **kw):
+    args = dict(key=A, key_row_stride=1024, value=B, value_row_stride=4096, k_cache=C, v_cache=C + 0x100000,
+                num_slots=4096, slot_mapping=A + 0x8000, num_tokens=4, num_kv_heads=8, head_dim=128,
+                cache_dtype=0, k_scale=None, v_scale=None, stream=None)
+    args.update(kw)
+    return lib.nva_store_kvcache(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(num_tokens=-1), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(num_kv_heads=0), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(cache_dtype=7), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(key=None), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(slot_mapping=None), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(key_row_stride=1000), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(num_slots=0), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(slot_mapping=A + 2), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(cache_dtype=1), _capi.NVA_ERR_INVALID_ARGUMENT),           # fp8 without scales
+    (dict(cache_dtype=1, k_scale=A, v_scale=B, key=A + 8), _capi.NVA_ERR_UNSUPPORTED),
+    (dict(key=A + 1), _capi.NVA_ERR_INVALID_ARGUMENT),               # bf16 misaligned
+])
+def test_store_rejects(lib, kw, code):
+    assert store(lib, **kw) == code
+    assert lib.nva_last_error().decode()
+
+
+def test_store_zero_tokens_is_noop(lib):
+    assert store(lib, num_tokens=0, key=None, value=None) == _capi.NVA_OK
+    assert lib.nva_last_error().decode() == ""
+
+
+def prefill(lib, **kw):
+    args = dict(q=A, q_row_stride=2048, k=B, k_row_stride=1024, v=C, v_row_stride=4096, block_table=None,
+                bt_row_stride=0, max_blocks=0, block_size=0, num_blocks=0, cu_q=A + 0x9000, cu_k=A + 0xA000,
+                num_seqs=2, max_seqlen_q=100, max_seqlen_k=100, num_heads=16, num_kv_heads=8, head_dim=128,
+                scale=0.088, out=C + 0x200000, out_row_stride=2048, stream=None)
+    args.update(kw)
+    return lib.nva_prefill(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(head_dim=64), _capi.NVA_ERR_UNSUPPORTED),
+    (dict(num_heads=12), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(num_seqs=-1), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(q=None), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(cu_k=None), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(q_row_stride=1024), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(v_row_stride=1000), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(q=A + 2), _capi.NVA_ERR_UNSUPPORTED),
+    (dict(scale=0.0), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(block_table=A, bt_row_stride=8, max_blocks=8, block_size=32, num_blocks=10), _capi.NVA_ERR_UNSUPPORTED),
+    (dict(block_table=A, bt_row_stride=4, max_blocks=8, block_size=256, num_blocks=10), _capi.NVA_ERR_INVALID_ARGUMENT),
+])
+def test_prefill_rejects(lib, kw, code):
+    assert prefill(lib, **kw) == code
+
+
+def test_prefill_empty_is_noop(lib):
+    assert prefill(lib, num_seqs=0, q=None) == _capi.NVA_OK
+    assert prefill(lib, max_seqlen_q=0) == _capi.NVA_OK
+
+
+def decode(lib, **kw):
+    args = dict(q=A, q_row_stride=2048, k_cache=B, v_cache=C, kv_dtype=0, k_scale=None, v_scale=None,
+                num_blocks=2048, seqlens=A + 0x9000, block_table=A + 0xA000, bt_row_stride=8, max_blocks=8,
+                block_size=256, batch=256, num_heads=16, num_kv_heads=8, head_dim=128, scale=0.088,
+                num_splits=0, out=C + 0x200000, out_row_stride=2048, workspace=None, workspace_bytes=0,
+                stream=None)
+    args.update(kw)
+    return lib.nva_decode(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(head_dim=64), _capi.NVA_ERR_UNSUPPORTED),
+    (dict(num_heads=24), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(num_heads=136), _capi.NVA_ERR_UNSUPPORTED),              # group 17
+    (dict(kv_dtype=3), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(kv_dtype=1), _capi.NVA_ERR_INVALID_ARGUMENT),            # fp8 without scales
+    (dict(batch=-2), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(block_size=48), _capi.NVA_ERR_UNSUPPORTED),
+    (dict(bt_row_stride=4), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(num_blocks=0), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(q=None), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(out=C + 8), _capi.NVA_ERR_UNSUPPORTED),
+    (dict(num_splits=-1), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(scale=-1.0), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(), _capi.NVA_ERR_WORKSPACE),                               # split-K needs a workspace
+    (dict(workspace=A, workspace_bytes=16), _capi.NVA_ERR_WORKSPACE),
+])
+def test_decode_rejects(lib, kw, code):
+    assert decode(lib, **kw) == code
+
+
+def test_decode_workspace_plan(lib):
+    f = lib.nva_decode_workspace_bytes
+    # one split -> no workspace
+    assert f(4, 16, 8, 128, 1, 256, 0, 0) == 0
+    assert f(256, 16, 8, 128, 8, 256, 0, 1) == 0
+    # explicit split count: ceil(8 / 2) = 4 pages per split -> 2 splits
+    assert f(256, 16, 8, 128, 8, 256, 0, 2) == 256 * 16 * 2 * (128 + 2) * 4
+    # heuristic: deterministic, depends only on sizes
+    a = f(256, 16, 8, 128, 8, 256, 0, 0)
+    assert a == f(256, 16, 8, 128, 8, 256, 0, 0) and a > 0
+    assert f(0, 16, 8, 128, 8, 256, 0, 0) == 0
+
+
+def test_decode_batch_zero_is_noop(lib):
+    assert decode(lib, batch=0, workspace=None) == _capi.NVA_OK
+
+
+def test_error_raises_runtime_error(lib):
+    assert decode(lib, head_dim=64) != 0
+    with pytest.raises(RuntimeError, match="head_dim"):
+        _capi.check(_capi.NVA_ERR_UNSUPPORTED)

@@ -1,0 +1,407 @@
+"""GPU parity of the HIP hot path against the CPU oracle (run on an MI355X).
+
+Bars: store_kvcache cache contents bit-exact; bf16 attention within max-abs 2e-2
+and mean-abs 2e-3 of the fp32 oracle; fp8-KV decode within 5e-2 of the oracle
+on the dequantised cache.  Every call goes through the C ABI of libnva_attn.so
+via the host mirror of the reference interface.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import (FP8_MAX_ABS, assert_attn_close, bits8, bits16, decode_reference, f32,
+                      prefill_reference, rows_of)
+from oracle import attention_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need an MI355X"
+    from nanovllm_amd import _capi
+    _capi.load()  # fail loudly if the HIP library is missing
+    return torch.device("cuda:0")
+
+
+def nva():
+    import nanovllm_amd as m
+    return m
+
+
+# ----------------------------------------------------------------------------
+# store_kvcache
+# ----------------------------------------------------------------------------
+
+def _sentinel_pool(case, dev, pattern=0x5A3C):
+    kc = torch.full(case.k_cache.shape, pattern, dtype=torch.int16, device=dev).view(torch.bfloat16)
+    vc = torch.full(case.v_cache.shape, pattern ^ 0x0F0F, dtype=torch.int16, device=dev).view(torch.bfloat16)
+    return kc, vc
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 4])
+def test_store_bitexact(dev, cfg):
+    from nanovllm_amd import workloads as W
+    case = W.CONFIGS[cfg]("cpu").to(dev)
+    if cfg in (1,):
+        key, value, slots = case.k_new, case.v_new, case.slot_mapping
+    else:
+        key, value, slots = case.k, case.v, case.slot_mapping
+    kc, vc = _sentinel_pool(case, dev)
+    ekc, evc = bits16(kc), bits16(vc)
+    O.store_kvcache(bits16(key), bits16(value), ekc, evc, slots.cpu().numpy())
+    nva().store_kvcache(key, value, kc, vc, slots)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(kc), ekc)
+    assert np.array_equal(bits16(vc), evc)
+
+
+def test_store_skips_out_of_range_slots(dev):
+    T, nkv, d, nb, bs = 40, 8, 128, 4, 16
+    g = torch.Generator(device=dev).manual_seed(3)
+    key = torch.randn(T, nkv, d, generator=g, device=dev).bfloat16()
+    value = torch.randn(T, nkv, d, generator=g, device=dev).bfloat16()
+    slots = torch.randperm(nb * bs, device=dev)[:T].int()
+    slots[::5] = -1
+    slots[3] = nb * bs  # one past the end
+    slots[7] = 1 << 30
+    kc = torch.zeros(nb, bs, nkv, d, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    ekc, evc = bits16(kc), bits16(vc)
+    O.store_kvcache(bits16(key), bits16(value), ekc, evc, slots.cpu().numpy())
+    nva().store_kvcache(key, value, kc, vc, slots)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(kc), ekc) and np.array_equal(bits16(vc), evc)
+
+
+@pytest.mark.parametrize("row_pad", [0, 1, 4, 3000])
+def test_store_unaligned_rows(dev, row_pad):
+    """Row strides that are not 16-byte multiples take narrower vector paths."""
+    T, nkv, d, nb, bs = 33, 2, 128, 3, 32
+    g = torch.Generator(device=dev).manual_seed(row_pad)
+    buf = torch.randn(T, nkv * d + row_pad, generator=g, device=dev).bfloat16()
+    key = buf[:, :nkv * d].view(T, nkv, d)
+    value = buf[:, row_pad:row_pad + nkv * d].view(T, nkv, d)
+    slots = torch.randperm(nb * bs, device=dev)[:T].int()
+    kc = torch.full((nb, bs, nkv, d), 7.0, dtype=torch.bfloat16, device=dev)
+    vc = torch.full_like(kc, -3.0)
+    ekc, evc = bits16(kc), bits16(vc)
+    O.store_kvcache(bits16(key), bits16(value), ekc, evc, slots.cpu().numpy())
+    nva().store_kvcache(key, value, kc, vc, slots)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(kc), ekc) and np.array_equal(bits16(vc), evc)
+
+
+def test_store_fp8_bitexact(dev):
+    """fp8 cache store == e4m3fn(x / scale) of the oracle and of torch's cast."""
+    T, nkv, d, nb, bs = 300, 8, 128, 4, 256
+    g = torch.Generator(device=dev).manual_seed(11)
+    key = (torch.randn(T, nkv, d, generator=g, device=dev) * 3).bfloat16()
+    value = (torch.randn(T, nkv, d, generator=g, device=dev) * 0.01).bfloat16()
+    # exercise ties, subnormals, the 448/464 boundary and overflow to NaN
+    key[0, 0, :8] = torch.tensor([464.0, 465.0, 480.0, -500.0, 448.0, 2 ** -10, 2 ** -9 * 1.5, 0.0])
+    k_scale = torch.linspace(0.5, 2.0, nkv, device=dev).float()
+    v_scale = (value.float().abs().amax(dim=(0, 2)) / 448).contiguous()
+    slots = torch.randperm(nb * bs, device=dev)[:T].int()
+    kc = torch.zeros(nb, bs, nkv, d, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    vc = torch.zeros_like(kc)
+    nva().store_kvcache(key, value, kc, vc, slots, k_scale, v_scale)
+    torch.cuda.synchronize()
+    ek = np.zeros((nb, bs, nkv, d), np.uint8)
+    ev = np.zeros_like(ek)
+    O.store_kvcache(O.quantize_e4m3fn(f32(key), f32(k_scale)), O.quantize_e4m3fn(f32(value), f32(v_scale)),
+                    ek, ev, slots.cpu().numpy())
+    assert np.array_equal(bits8(kc), ek)
+    assert np.array_equal(bits8(vc), ev)
+    torch_k = (key.float().cpu() / k_scale.cpu().view(1, nkv, 1)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    got_rows = bits8(kc).reshape(-1, nkv, d)[slots.cpu().numpy()]
+    assert np.array_equal(got_rows, torch_k)
+
+
+# ----------------------------------------------------------------------------
+# decode
+# ----------------------------------------------------------------------------
+
+def _run_decode(case, num_splits=0, store=True):
+    m = nva()
+    if store:
+        m.store_kvcache(case.k_new, case.v_new, case.k_cache, case.v_cache, case.slot_mapping,
+                        case.k_scale, case.v_scale)
+    o = m.flash_attn_with_kvcache(case.q.unsqueeze(1), case.k_cache, case.v_cache, case.context_lens,
+                                  case.block_tables, case.scale, True, num_splits=num_splits,
+                                  k_scale=case.k_scale, v_scale=case.v_scale)
+    torch.cuda.synchronize()
+    return f32(o[:, 0])
+
+
+@pytest.mark.parametrize("num_splits", [0, 1, 2, 3])
+def test_decode_cfg1(dev, num_splits):
+    from nanovllm_amd import workloads as W
+    case = W.config1("cpu").to(dev)
+    got = _run_decode(case, num_splits)
+    assert_attn_close(got, decode_reference(case), what=f"cfg1 splits={num_splits}")
+
+
+def test_decode_cfg3_full(dev):
+    from nanovllm_amd import workloads as W
+    case = W.config3(dev)
+    got = _run_decode(case)
+    mx, mn = assert_attn_close(got, decode_reference(case), what="cfg3")
+    print(f"cfg3 decode max-abs {mx:.3e} mean-abs {mn:.3e}")
+
+
+def test_decode_cfg3_split_invariance(dev):
+    from nanovllm_amd import workloads as W
+    case = W.config3(dev)
+    a = _run_decode(case, 0)
+    b = _run_decode(case, 1, store=False)
+    c = _run_decode(case, 8, store=False)
+    assert np.abs(a - b).max() <= 1e-2 and np.abs(a - c).max() <= 1e-2
+
+
+def test_decode_cfg5_fp8(dev):
+    from nanovllm_amd import workloads as W
+    case = W.config5(dev)
+    got = _run_decode(case)
+    seqs = [0, 1, 17, 33, 48, 63]
+    ref = decode_reference(case, seqs)
+    mx, mn = assert_attn_close(got[seqs], ref, max_abs=FP8_MAX_ABS, mean_abs=FP8_MAX_ABS, what="cfg5 fp8")
+    print(f"cfg5 fp8 decode max-abs {mx:.3e} mean-abs {mn:.3e}")
+
+
+@pytest.mark.parametrize("nh,nkv", [(8, 8), (16, 8), (32, 8), (64, 8), (16, 1), (128, 8)])
+@pytest.mark.parametrize("fp8", [False, True])
+def test_decode_group_sizes(dev, nh, nkv, fp8):
+    from nanovllm_amd import workloads as W
+    lengths = [1, 2, 31, 32, 33, 255, 256, 257, 700, 1025]
+    case = W.make_decode_case(len(lengths), nh, nkv, 0, 0, 40, fp8=fp8, seed=nh * 10 + nkv, bulk_device=dev,
+                              lengths=lengths, table_width=6)
+    for ns in (0, 1, 4):
+        got = _run_decode(case, ns, store=(ns == 0))
+        tol = dict(max_abs=FP8_MAX_ABS, mean_abs=FP8_MAX_ABS) if fp8 else {}
+        assert_attn_close(got, decode_reference(case), what=f"nh={nh} nkv={nkv} fp8={fp8} splits={ns}", **tol)
+
+
+def test_decode_zero_and_single_key(dev):
+    from nanovllm_amd import workloads as W
+    lengths = [0, 1, 5, 0]
+    case = W.make_decode_case(4, 16, 8, 0, 0, 8, seed=5, bulk_device=dev, lengths=lengths, table_width=2)
+    got = _run_decode(case, store=False)
+    assert np.all(got[0] == 0) and np.all(got[3] == 0)
+    # one key: o = v0 exactly (p = 1, l = 1)
+    v0 = f32(case.v_cache[case.block_tables[1, 0].long(), 0])  # (nkv, d)
+    assert np.array_equal(got[1], np.repeat(v0, 2, axis=0))
+
+
+def test_decode_fp8_all_codes(dev):
+    """ctx = 1 with v_scale = 1: the output is the e4m3fn value of each V code,
+    exactly (every e4m3fn value is a bf16 value)."""
+    nkv, d, bs = 2, 128, 32
+    codes = torch.arange(256, dtype=torch.uint8, device=dev).view(1, 1, nkv, d)
+    kc = torch.zeros(1, bs, nkv, d, dtype=torch.uint8, device=dev)
+    vc = torch.zeros_like(kc)
+    vc[:, 0] = codes[0]
+    q = torch.randn(1, 1, 2 * nkv, d, device=dev).bfloat16()
+    one = torch.ones(nkv, dtype=torch.float32, device=dev)
+    o = nva().flash_attn_with_kvcache(q, kc.view(torch.float8_e4m3fn), vc.view(torch.float8_e4m3fn),
+                                      torch.ones(1, dtype=torch.int32, device=dev),
+                                      torch.zeros(1, 1, dtype=torch.int32, device=dev), 0.1,
+                                      k_scale=one, v_scale=one)
+    torch.cuda.synchronize()
+    got = f32(o[0, 0]).reshape(nkv, 2, d)[:, 0].reshape(-1)  # head 2h reads kv head h
+    expect = O.e4m3fn_table().astype(np.float32)
+    nan = np.isnan(expect)
+    assert np.array_equal(got[~nan], expect[~nan])
+    assert np.isnan(got[nan]).all()
+
+
+def test_decode_inconsistent_table_is_safe(dev):
+    """-1 / out-of-range block ids inside the visible range are masked, not read."""
+    from nanovllm_amd import workloads as W
+    case = W.make_decode_case(2, 16, 8, 0, 0, 8, seed=9, bulk_device=dev, lengths=[600, 300], table_width=3)
+    bt = case.block_tables.clone()
+    bt[0, 1] = -1
+    bt[1, 1] = 1 << 20
+    o = nva().flash_attn_with_kvcache(case.q.unsqueeze(1), case.k_cache, case.v_cache, case.context_lens,
+                                      bt, case.scale)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o.float()).all()
+    # seq 1 keeps only its first page's 256 keys
+    case.context_lens = torch.tensor([600, 256], dtype=torch.int32, device=dev)
+    ref = decode_reference(case, [1])
+    assert_attn_close(f32(o[1:, 0]), ref, what="masked page")
+
+
+# ----------------------------------------------------------------------------
+# prefill
+# ----------------------------------------------------------------------------
+
+def _run_prefill(case, store=True):
+    m = nva()
+    if store:
+        m.store_kvcache(case.k, case.v, case.k_cache, case.v_cache, case.slot_mapping)
+    if case.block_tables is None:
+        k, v = case.k, case.v
+    else:
+        k, v = case.k_cache, case.v_cache
+    o = m.flash_attn_varlen_func(case.q, k, v, case.max_seqlen_q, case.cu_seqlens_q, case.max_seqlen_k,
+                                 case.cu_seqlens_k, case.scale, True, case.block_tables)
+    torch.cuda.synchronize()
+    return f32(o)
+
+
+def test_prefill_cfg2(dev):
+    from nanovllm_amd import workloads as W
+    case = W.config2("cpu").to(dev)
+    got = _run_prefill(case)
+    mx, mn = assert_attn_close(got, prefill_reference(case), what="cfg2")
+    print(f"cfg2 prefill max-abs {mx:.3e} mean-abs {mn:.3e}")
+
+
+def test_prefill_cfg4_prefix(dev):
+    from nanovllm_amd import workloads as W
+    case = W.config4("cpu").to(dev)
+    got = _run_prefill(case)
+    seqs = [0, 5, 10, 15]
+    ref = prefill_reference(case, seqs)
+    mx, mn = assert_attn_close(got[rows_of(case, seqs)], ref, what="cfg4")
+    print(f"cfg4 prefill max-abs {mx:.3e} mean-abs {mn:.3e}")
+
+
+@pytest.mark.parametrize("nh,nkv", [(16, 16), (16, 8), (32, 8), (64, 8), (14, 2)])
+def test_prefill_shapes(dev, nh, nkv):
+    from nanovllm_amd import workloads as W
+    lens = [1, 63, 64, 65, 128, 129, 300, 0, 17]
+    case = W.make_prefill_case(lens, nh, nkv, 16, seed=nh + nkv, bulk_device=dev, block_size=256)
+    got = _run_prefill(case)
+    assert_attn_close(got, prefill_reference(case), what=f"prefill nh={nh} nkv={nkv}")
+
+
+@pytest.mark.parametrize("prefix", [256, 512])
+@pytest.mark.parametrize("shared", [True, False])
+def test_prefill_prefix_shapes(dev, prefix, shared):
+    from nanovllm_amd import workloads as W
+    lens = [1, 100, 256, 0, 333]
+    case = W.make_prefill_case(lens, 16, 8, 40, prefix_len=prefix, seed=prefix + shared, bulk_device=dev,
+                               shared_prefix=shared)
+    got = _run_prefill(case)
+    assert_attn_close(got, prefill_reference(case), what=f"prefix={prefix} shared={shared}")
+
+
+def test_prefill_prefix_equals_full_tail(dev):
+    """Prefix-cached prefill == the last Lq rows of a full prefill over prefix+suffix."""
+    from nanovllm_amd import workloads as W
+    m = nva()
+    lens = [300, 129]
+    case = W.make_prefill_case(lens, 16, 8, 16, prefix_len=256, seed=77, bulk_device=dev, shared_prefix=False)
+    got = _run_prefill(case)
+    bs = case.block_size
+    for s, Lq in enumerate(lens):
+        Lk = 256 + Lq
+        bt = case.block_tables[s]
+        pages = bt[: math.ceil(Lk / bs)].long()
+        k_full = case.k_cache.index_select(0, pages).reshape(-1, 8, 128)[:Lk].contiguous()
+        v_full = case.v_cache.index_select(0, pages).reshape(-1, 8, 128)[:Lk].contiguous()
+        q_full = torch.cat([torch.randn(256, 16, 128, device=dev).bfloat16(),
+                            case.q[case.cu_seqlens_q[s]:case.cu_seqlens_q[s + 1]]])
+        cu = torch.tensor([0, Lk], dtype=torch.int32, device=dev)
+        full = m.flash_attn_varlen_func(q_full, k_full, v_full, Lk, cu, Lk, cu, case.scale)
+        torch.cuda.synchronize()
+        rows = rows_of(case, [s])
+        assert np.abs(f32(full[256:]) - got[rows]).max() <= 1e-2
+
+
+# ----------------------------------------------------------------------------
+# the Attention module behind the Context, and graph capture
+# ----------------------------------------------------------------------------
+
+def test_attention_module_prefill_then_decode(dev):
+    from nanovllm_amd import workloads as W
+    m = nva()
+    nh, nkv, d, bs = 16, 8, 128, 256
+    lens = [200, 513]
+    case = W.make_prefill_case(lens, nh, nkv, 8, seed=21, bulk_device=dev)
+    attn = m.Attention(nh, d, d ** -0.5, nkv)
+    attn.k_cache, attn.v_cache = case.k_cache, case.v_cache
+    m.set_context(True, case.cu_seqlens_q, case.cu_seqlens_k, case.max_seqlen_q, case.max_seqlen_k,
+                  case.slot_mapping, None, None)
+    o = attn(case.q.reshape(-1, nh * d), case.k.reshape(-1, nkv * d), case.v.reshape(case.v.shape[0], -1))
+    torch.cuda.synchronize()
+    assert o.shape == (sum(lens), nh * d)
+    assert_attn_close(f32(o).reshape(-1, nh, d), prefill_reference(case), what="module prefill")
+    # one decode step per sequence; the page table is read back from the prefill's
+    # slot mapping (page i of sequence s holds its tokens i*bs .. i*bs+bs-1), and
+    # the new token (position L, L % bs != 0 here) goes to the next slot of the last page
+    bt = torch.full((2, 3), -1, dtype=torch.int32)
+    slots = case.slot_mapping.cpu().tolist()
+    cu = case.cu_seqlens_q.cpu().tolist()
+    ctx, new_slots = [], []
+    for s, L in enumerate(lens):
+        seq_slots = slots[cu[s]:cu[s + 1]]
+        pages = [seq_slots[i] // bs for i in range(0, L, bs)]
+        bt[s, :len(pages)] = torch.tensor(pages, dtype=torch.int32)
+        ctx.append(L + 1)
+        assert L % bs
+        new_slots.append(pages[-1] * bs + L % bs)
+    g = torch.Generator(device=dev).manual_seed(4)
+    q1 = torch.randn(2, nh * d, generator=g, device=dev).bfloat16()
+    k1 = torch.randn(2, nkv * d, generator=g, device=dev).bfloat16()
+    v1 = torch.randn(2, nkv * d, generator=g, device=dev).bfloat16()
+    m.set_context(False, slot_mapping=torch.tensor(new_slots, dtype=torch.int32, device=dev),
+                  context_lens=torch.tensor(ctx, dtype=torch.int32, device=dev), block_tables=bt.to(dev))
+    o1 = attn(q1, k1, v1)
+    torch.cuda.synchronize()
+    m.reset_context()
+    for s, L in enumerate(lens):
+        k_all = torch.cat([case.k[cu[s]:cu[s + 1]], k1[s].view(1, nkv, d)])
+        v_all = torch.cat([case.v[cu[s]:cu[s + 1]], v1[s].view(1, nkv, d)])
+        ref = O.attention(f32(q1[s]).reshape(1, nh, d), f32(k_all), f32(v_all), d ** -0.5)[0]
+        assert_attn_close(f32(o1[s]).reshape(nh, d), ref, what=f"module decode seq {s}")
+
+
+def test_decode_graph_capture_replay(dev):
+    """store + decode captured in one graph, replayed with new inputs copied into the
+    static buffers (model_runner.py:266-282); every replay matches eager."""
+    from nanovllm_amd import workloads as W
+    m = nva()
+    case = W.make_decode_case(16, 16, 8, 50, 900, 64, seed=31, bulk_device=dev, table_width=4)
+    st = {k: getattr(case, k).clone() for k in ("q", "context_lens", "block_tables", "slot_mapping")}
+    k_new, v_new = case.k_new.clone(), case.v_new.clone()
+    kc_eager, vc_eager = case.k_cache.clone(), case.v_cache.clone()
+
+    def step(q, kn, vn, kc, vc, lens, bt, slots):
+        m.store_kvcache(kn, vn, kc, vc, slots)
+        return m.flash_attn_with_kvcache(q.unsqueeze(1), kc, vc, lens, bt, case.scale)
+
+    step(st["q"], k_new, v_new, case.k_cache, case.v_cache, st["context_lens"], st["block_tables"],
+         st["slot_mapping"])  # warmup
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step(st["q"], k_new, v_new, case.k_cache, case.v_cache, st["context_lens"], st["block_tables"],
+                   st["slot_mapping"])
+    g = torch.Generator(device=dev).manual_seed(99)
+    for rep in range(4):
+        q = torch.randn(st["q"].shape, generator=g, device=dev).bfloat16()
+        kn = torch.randn(k_new.shape, generator=g, device=dev).bfloat16()
+        vn = torch.randn(v_new.shape, generator=g, device=dev).bfloat16()
+        lens = torch.randint(1, 900, (16,), generator=g, device=dev).int()
+        lens = torch.minimum(lens, case.context_lens)  # stay inside the allocated pages
+        bt = case.block_tables
+        slots = torch.tensor([int(bt[b, (int(L) - 1) // 256]) * 256 + (int(L) - 1) % 256
+                              for b, L in enumerate(lens.cpu().tolist())], dtype=torch.int32, device=dev)
+        st["q"].copy_(q)
+        k_new.copy_(kn)
+        v_new.copy_(vn)
+        st["context_lens"].copy_(lens)
+        st["slot_mapping"].copy_(slots)
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = step(q, kn, vn, kc_eager, vc_eager, lens, bt, slots)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep} differs from eager"
+        assert torch.equal(case.k_cache, kc_eager) and torch.equal(case.v_cache, vc_eager)
