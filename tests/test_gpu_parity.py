@@ -371,7 +371,6 @@ def test_decode_graph_capture_replay(dev):
     case = W.make_decode_case(16, 16, 8, 50, 900, 64, seed=31, bulk_device=dev, table_width=4)
     st = {k: getattr(case, k).clone() for k in ("q", "context_lens", "block_tables", "slot_mapping")}
     k_new, v_new = case.k_new.clone(), case.v_new.clone()
-    kc_eager, vc_eager = case.k_cache.clone(), case.v_cache.clone()
 
     def step(q, kn, vn, kc, vc, lens, bt, slots):
         m.store_kvcache(kn, vn, kc, vc, slots)
@@ -380,6 +379,7 @@ def test_decode_graph_capture_replay(dev):
     step(st["q"], k_new, v_new, case.k_cache, case.v_cache, st["context_lens"], st["block_tables"],
          st["slot_mapping"])  # warmup
     torch.cuda.synchronize()
+    kc_eager, vc_eager = case.k_cache.clone(), case.v_cache.clone()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         out = step(st["q"], k_new, v_new, case.k_cache, case.v_cache, st["context_lens"], st["block_tables"],
