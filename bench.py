@@ -153,6 +153,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["decode", "prefill", "fp8"], default=None)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 1 GiB device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the attention path has no cross-GPU step here "
@@ -165,6 +167,14 @@ def main(argv=None):
     dev = torch.device("cuda:0")
     steps, warmup = args.steps, args.warmup
     out = {}
+    if args.copy_probe:
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("[bench] copy probe: 3 x 1 GiB device-to-device copies")
+        del src, dst
 
     if args.only in (None, "decode"):
         log("[bench] config 3: decode step (store + paged decode), B=256")

@@ -165,12 +165,16 @@ int nva_prefill(const void* q, int64_t q_row_stride, const void* k, int64_t k_ro
 int64_t nva_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                    int32_t max_blocks_per_seq, int32_t block_size, int32_t kv_dtype,
                                    int32_t num_splits) {
-  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks_per_seq <= 0 || head_dim <= 0) return 0;
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks_per_seq <= 0 || head_dim <= 0 ||
+      block_size <= 0 || num_splits < 0)
+    return 0;
   const nva::DecodePlan plan =
       nva::plan_decode(batch, num_kv_heads, max_blocks_per_seq, block_size, kv_dtype, num_splits);
-  if (plan.num_splits <= 1) return 0;
-  const int64_t rows = static_cast<int64_t>(batch) * num_heads * plan.num_splits;
-  return rows * head_dim * 4 + rows * 2 * 4;
+  if (plan.partial_slots <= 0) return 0;
+  const int64_t rows = plan.partial_slots * num_heads;
+  int64_t bytes = rows * head_dim * 4 + rows * 2 * 4;
+  if (plan.balanced_ranges > 0) bytes += (static_cast<int64_t>(batch) + 1) * 4;
+  return (bytes + 255) & ~static_cast<int64_t>(255);
 }
 
 int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache, int32_t kv_dtype,
@@ -232,9 +236,12 @@ int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const v
   p.seqlens = cache_seqlens;
   p.block_table = block_table;
   p.out = static_cast<uint16_t*>(out);
-  const int64_t rows = static_cast<int64_t>(batch) * num_heads * plan.num_splits;
+  const int64_t rows = plan.partial_slots * num_heads;
   p.ws_o = need > 0 ? static_cast<float*>(workspace) : nullptr;
   p.ws_ml = need > 0 ? static_cast<float*>(workspace) + rows * head_dim : nullptr;
+  p.ws_prefix = need > 0 && plan.balanced_ranges > 0
+                    ? reinterpret_cast<int32_t*>(static_cast<float*>(workspace) + rows * (head_dim + 2))
+                    : nullptr;
   p.q_row_stride = q_row_stride;
   p.out_row_stride = out_row_stride;
   p.bt_row_stride = bt_row_stride;
@@ -247,6 +254,7 @@ int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const v
   p.group = num_heads / num_kv_heads;
   p.keys_per_split = plan.pages_per_split * block_size;
   p.num_splits = plan.num_splits;
+  p.balanced_ranges = plan.balanced_ranges;
   p.scale_log2 = softmax_scale * kLog2e;
   return hip_status(nva::launch_decode(p, kv_dtype, static_cast<hipStream_t>(stream)), "decode launch");
 }

@@ -33,8 +33,9 @@ struct DecodeParams {
   const int32_t* seqlens;     // [B]
   const int32_t* block_table; // [B, bt_row_stride]
   uint16_t* out;              // (B, nh, 128) bf16
-  float* ws_o;                // [B, nh, num_splits, 128] partial numerators
-  float* ws_ml;               // [B, nh, num_splits, 2] partial (max, sum)
+  float* ws_o;                // [slots, nh, 128] partial numerators
+  float* ws_ml;               // [slots, nh, 2] partial (max, sum)
+  int32_t* ws_prefix;         // [B + 1] step prefix (balanced mode)
   int64_t q_row_stride;
   int64_t out_row_stride;
   int64_t bt_row_stride;
@@ -45,8 +46,9 @@ struct DecodeParams {
   int32_t num_heads;
   int32_t num_kv_heads;
   int32_t group;              // num_heads / num_kv_heads
-  int32_t keys_per_split;     // multiple of block_size
-  int32_t num_splits;
+  int32_t keys_per_split;     // fixed mode: multiple of block_size
+  int32_t num_splits;         // fixed mode: splits per sequence
+  int32_t balanced_ranges;    // balanced mode: number of step ranges P (0 = fixed mode)
   float scale_log2;           // softmax_scale * log2(e)
 };
 
@@ -79,9 +81,13 @@ hipError_t launch_decode(const DecodeParams& p, int kv_dtype, hipStream_t stream
 hipError_t launch_prefill(const PrefillParams& p, int max_seqlen_q, hipStream_t stream);
 
 // Split-K plan shared by nva_decode and nva_decode_workspace_bytes.
+// balanced_ranges > 0: balanced mode with that many step ranges; otherwise
+// fixed mode with num_splits splits of pages_per_split pages per sequence.
 struct DecodePlan {
   int32_t pages_per_split;
   int32_t num_splits;
+  int32_t balanced_ranges;
+  int64_t partial_slots;      // partial (O, max, sum) slots the workspace holds
 };
 DecodePlan plan_decode(int32_t batch, int32_t num_kv_heads, int32_t max_blocks,
                        int32_t block_size, int32_t kv_dtype, int32_t requested_splits);

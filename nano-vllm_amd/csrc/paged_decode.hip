@@ -88,34 +88,169 @@ __device__ __forceinline__ void fp8x16_to_ops(u32x4 w, bf16x8& lo, bf16x8& hi) {
 
 }  // namespace
 
+// Raw loads of one 32-key step for one kv head (see the file comment for the
+// lane layout).  bf16: K tile rows as 16-byte MFMA operands, 8 value rows of 8
+// columns; fp8: the same positions, half the bytes.
 template <bool FP8>
-__global__ __launch_bounds__(64) void paged_decode_kernel(DecodeParams p) {
+struct StepRegs;
+template <>
+struct StepRegs<false> {
+  u32x4 k[2][4];
+  u32x4 v[8];
+};
+template <>
+struct StepRegs<true> {
+  u32x4 k[2][2];
+  u32x2 v[8];
+};
+
+// Per-wave constants of a work item.
+struct WaveItem {
+  const char* kbase;      // k_cache + kv head offset (bytes)
+  const char* vbase;
+  int64_t slot_bytes;     // bytes between consecutive slots
+  const int32_t* bt;      // block table row of the sequence
+  int64_t num_blocks;
+  int block_size;
+  int k_begin;
+  int k_end;
+  int krow0;              // K tile row this lane supplies (tile 0)
+  int n;                  // lane % 16
+  int g;                  // lane / 16
+};
+
+// Slot of the first key of step i and how many of its 32 keys exist (0 when the
+// block id is outside the pool: those keys stay masked and nothing is read from
+// the bad page).
+__device__ __forceinline__ int64_t step_row(const WaveItem& w, int i, int& nvalid) {
+  const int key0 = w.k_begin + 32 * i;
+  const int blk = key0 / w.block_size;
+  const int page = w.bt[blk];
+  const bool ok = page >= 0 && page < w.num_blocks;
+  nvalid = ok ? min(32, w.k_end - key0) : 0;
+  return static_cast<int64_t>(ok ? page : 0) * w.block_size + (key0 - blk * w.block_size);
+}
+
+template <bool FP8>
+__device__ __forceinline__ void load_step(StepRegs<FP8>& r, const WaveItem& w, int64_t row0) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const char* rp = w.kbase + (row0 + w.krow0 + 4 * t) * w.slot_bytes;
+    if constexpr (!FP8) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) r.k[t][s] = ld16(rp + qk_dim<false>(s, w.g) * 2);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) r.k[t][u] = ld16(rp + 64 * u + 16 * w.g);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const char* rp = w.vbase + (row0 + 8 * w.g + i) * w.slot_bytes;
+    if constexpr (!FP8)
+      r.v[i] = ld16(rp + 16 * w.n);
+    else
+      r.v[i] = ld8(rp + 8 * w.n);
+  }
+}
+
+// Online-softmax update of one step: scores, running max/sum, O^T += V^T P^T.
+template <bool FP8>
+__device__ __forceinline__ void compute_step(StepRegs<FP8>& r, int nvalid, int g, const bf16x8 (&qop)[4],
+                                             float sl2, f32x4 (&acc)[8], float& m_run, float& l_run) {
+  if (nvalid < 32) {  // keys past the end (or on a bad page) contribute nothing
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (8 * g + i >= nvalid) {
+        if constexpr (!FP8)
+          r.v[i] = u32x4{0u, 0u, 0u, 0u};
+        else
+          r.v[i] = u32x2{0u, 0u};
+      }
+  }
+  bf16x8 kop[2][4];
+  if constexpr (!FP8) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kop[t][s] = as_bf16x8(r.k[t][s]);
+  } else {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      fp8x16_to_ops(r.k[t][0], kop[t][0], kop[t][1]);
+      fp8x16_to_ops(r.k[t][1], kop[t][2], kop[t][3]);
+    }
+  }
+  f32x4 st[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    st[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) st[t] = mfma16x16x32(kop[t][s], qop[s], st[t]);
+  }
+  float sv[8];
+  float mx = kNegInf;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float x = st[i >> 2][i & 3] * sl2;
+    sv[i] = (8 * g + i < nvalid) ? x : kNegInf;
+    mx = fmaxf(mx, sv[i]);
+  }
+  mx = fmaxf(mx, shfl_xor(mx, 16));
+  mx = fmaxf(mx, shfl_xor(mx, 32));
+  const float m_new = fmaxf(m_run, mx);
+  const float m_use = m_new == kNegInf ? 0.f : m_new;  // a step with no valid key changes nothing
+  const float alpha = fast_exp2(m_run - m_use);
+  m_run = m_new;
+  float psum = 0.f;
+  float pv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    pv[i] = fast_exp2(sv[i] - m_use);
+    psum += pv[i];
+  }
+  l_run = l_run * alpha + psum;
+  u32x4 pw;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) pw[w] = pack_bf16x2(pv[2 * w], pv[2 * w + 1]);
+  const bf16x8 pop = as_bf16x8(pw);
+  bf16x8 vt[8];
+  if constexpr (!FP8)
+    transpose_v_bf16(r.v, vt);
+  else
+    transpose_v_fp8(r.v, vt);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    acc[j] *= alpha;
+    acc[j] = mfma16x16x32(vt[j], pop, acc[j]);
+  }
+}
+
+// One wave, one kv head: attention of the head group's queries over keys
+// [k_begin, k_end) of sequence b.  Writes the normalised output when `direct`,
+// otherwise the unnormalised partial (O * v_scale, running max, sum) at `slot`.
+template <bool FP8, bool PREFETCH>
+__device__ __forceinline__ void decode_segment(const DecodeParams& p, int kvh, int b, int k_begin, int k_end,
+                                               bool direct, int64_t slot) {
   constexpr int EB = FP8 ? 1 : 2;  // bytes per cache element
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
   const int n = lane & 15;
   const int g = lane >> 4;
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
-  const int G = p.group;
-  const int h = kvh * G + n;
-  const bool head_ok = n < G;
-  const bool direct = p.num_splits == 1;
+  const int h = kvh * p.group + n;
+  const bool head_ok = n < p.group;
 
-  int ctx = p.seqlens[b];
-  const int cap = p.max_blocks * p.block_size;
-  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
-  const int k_begin = split * p.keys_per_split;
-  const int k_end = min(ctx, k_begin + p.keys_per_split);
-  if (k_begin >= k_end) {
-    if (direct && head_ok) {
-      uint16_t* orow = p.out + b * p.out_row_stride + h * kHeadDim + 32 * g;
-      const u32x4 z = {0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) st16(orow + 8 * r, z);
-    }
-    return;
-  }
+  WaveItem w;
+  w.slot_bytes = static_cast<int64_t>(p.num_kv_heads) * kHeadDim * EB;
+  w.kbase = static_cast<const char*>(p.k_cache) + static_cast<int64_t>(kvh) * kHeadDim * EB;
+  w.vbase = static_cast<const char*>(p.v_cache) + static_cast<int64_t>(kvh) * kHeadDim * EB;
+  w.bt = p.block_table + b * p.bt_row_stride;
+  w.num_blocks = p.num_blocks;
+  w.block_size = p.block_size;
+  w.k_begin = k_begin;
+  w.k_end = k_end;
+  w.krow0 = 8 * (n >> 2) + (n & 3);  // K tile row n of tile t holds key 8*(n/4) + 4*t + n%4
+  w.n = n;
+  w.g = g;
 
   // Q^T operand: head n, 8 contraction elements per MFMA.
   bf16x8 qop[4];
@@ -127,11 +262,6 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeParams p) {
       qop[s] = as_bf16x8(head_ok ? ld16(qrow + qk_dim<FP8>(s, g)) : z);
     }
   }
-
-  const int64_t slot_bytes = static_cast<int64_t>(p.num_kv_heads) * kHeadDim * EB;
-  const char* kbase = static_cast<const char*>(p.k_cache) + static_cast<int64_t>(kvh) * kHeadDim * EB;
-  const char* vbase = static_cast<const char*>(p.v_cache) + static_cast<int64_t>(kvh) * kHeadDim * EB;
-  const int32_t* bt = p.block_table + b * p.bt_row_stride;
   const float sl2 = FP8 ? p.scale_log2 * p.k_scale[kvh] : p.scale_log2;
 
   f32x4 acc[8];
@@ -140,106 +270,24 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeParams p) {
   float m_run = kNegInf;
   float l_run = 0.f;
 
-  // K tile row n of tile t holds key 8*(n/4) + 4*t + (n%4) of the step.
-  const int krow0 = 8 * (n >> 2) + (n & 3);
-  const int bs = p.block_size;
-
-  for (int blk = k_begin / bs; blk * bs < k_end; ++blk) {
-    const int page = bt[blk];
-    if (page < 0 || page >= p.num_blocks) continue;  // inconsistent table: keys stay masked
-    const int kp_end = min(k_end, (blk + 1) * bs);
-    for (int key0 = blk * bs; key0 < kp_end; key0 += 32) {
-      const int64_t row0 = static_cast<int64_t>(page) * bs + (key0 - blk * bs);
-      const int nvalid = kp_end - key0;  // keys of this step that exist (may exceed 32)
-
-      // ---- loads ---------------------------------------------------------
-      bf16x8 kop[2][4];
-      bf16x8 vt[8];
-      if constexpr (!FP8) {
-        u32x4 kr[2][4];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const char* rp = kbase + (row0 + krow0 + 4 * t) * slot_bytes;
-#pragma unroll
-          for (int s = 0; s < 4; ++s) kr[t][s] = ld16(rp + qk_dim<false>(s, g) * 2);
-        }
-        u32x4 vr[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) vr[i] = ld16(vbase + (row0 + 8 * g + i) * slot_bytes + 16 * n);
-        if (nvalid < 32) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            if (8 * g + i >= nvalid) vr[i] = u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int s = 0; s < 4; ++s) kop[t][s] = as_bf16x8(kr[t][s]);
-        transpose_v_bf16(vr, vt);
-      } else {
-        u32x4 kr[2][2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const char* rp = kbase + (row0 + krow0 + 4 * t) * slot_bytes;
-#pragma unroll
-          for (int u = 0; u < 2; ++u) kr[t][u] = ld16(rp + 64 * u + 16 * g);
-        }
-        u32x2 vr[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) vr[i] = ld8(vbase + (row0 + 8 * g + i) * slot_bytes + 8 * n);
-        if (nvalid < 32) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            if (8 * g + i >= nvalid) vr[i] = u32x2{0u, 0u};
-        }
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          fp8x16_to_ops(kr[t][0], kop[t][0], kop[t][1]);
-          fp8x16_to_ops(kr[t][1], kop[t][2], kop[t][3]);
-        }
-        transpose_v_fp8(vr, vt);
+  // Two register buffers: with PREFETCH the loads of step i+1 are in flight
+  // while step i is computed.
+  const int nsteps = (k_end - k_begin + 31) >> 5;
+  if (nsteps > 0) {
+    StepRegs<FP8> A, B;
+    int nvA = 0, nvB = 0;
+    load_step<FP8>(A, w, step_row(w, 0, nvA));
+    for (int i = 0; i < nsteps; i += 2) {
+      const bool has1 = i + 1 < nsteps;
+      const bool has2 = i + 2 < nsteps;
+      if (PREFETCH && has1) load_step<FP8>(B, w, step_row(w, i + 1, nvB));
+      compute_step<FP8>(A, nvA, g, qop, sl2, acc, m_run, l_run);
+      if (has1) {
+        if (!PREFETCH) load_step<FP8>(B, w, step_row(w, i + 1, nvB));
+        if (PREFETCH && has2) load_step<FP8>(A, w, step_row(w, i + 2, nvA));
+        compute_step<FP8>(B, nvB, g, qop, sl2, acc, m_run, l_run);
       }
-
-      // ---- scores ----------------------------------------------------------
-      f32x4 st[2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        st[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) st[t] = mfma16x16x32(kop[t][s], qop[s], st[t]);
-      }
-      float sv[8];
-      float mx = kNegInf;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float x = st[i >> 2][i & 3] * sl2;
-        sv[i] = (8 * g + i < nvalid) ? x : kNegInf;
-        mx = fmaxf(mx, sv[i]);
-      }
-      mx = fmaxf(mx, shfl_xor(mx, 16));
-      mx = fmaxf(mx, shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);  // finite: key0 itself is valid
-      const float alpha = fast_exp2(m_run - m_new);
-      m_run = m_new;
-      float psum = 0.f;
-      float pv[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        pv[i] = fast_exp2(sv[i] - m_new);
-        psum += pv[i];
-      }
-      l_run = l_run * alpha + psum;
-      u32x4 pw;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) pw[w] = pack_bf16x2(pv[2 * w], pv[2 * w + 1]);
-      const bf16x8 pop = as_bf16x8(pw);
-
-      // ---- O^T += V^T . P^T ---------------------------------------------
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        acc[j] *= alpha;
-        acc[j] = mfma16x16x32(vt[j], pop, acc[j]);
-      }
+      if (!PREFETCH && has2) load_step<FP8>(A, w, step_row(w, i + 2, nvA));
     }
   }
 
@@ -255,11 +303,11 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeParams p) {
     for (int r = 0; r < 4; ++r) {
       u32x4 o;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) o[w] = pack_bf16x2(acc[2 * w][r] * inv, acc[2 * w + 1][r] * inv);
+      for (int q2 = 0; q2 < 4; ++q2) o[q2] = pack_bf16x2(acc[2 * q2][r] * inv, acc[2 * q2 + 1][r] * inv);
       st16(orow + 8 * r, o);
     }
   } else {
-    const int64_t idx = (static_cast<int64_t>(b) * p.num_heads + h) * p.num_splits + split;
+    const int64_t idx = slot * p.num_heads + h;
     float* wo = p.ws_o + idx * kHeadDim + 32 * g;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -279,74 +327,291 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeParams p) {
   }
 }
 
-// Log-sum-exp merge of the split partials: one wavefront per (sequence, head),
-// two output columns per lane.
+__device__ __forceinline__ int clamped_len(const DecodeParams& p, int b) {
+  const int ctx = p.seqlens[b];
+  const int cap = p.max_blocks * p.block_size;
+  return ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+}
+
+// ---------------------------------------------------------------------------
+// Fixed split-K: workgroup = WAVES kv heads of one sequence over one split of
+// keys_per_split keys.  Grid: (head groups, splits, batch).  Partial slot of
+// split s of sequence b: b * num_splits + s.
+// ---------------------------------------------------------------------------
+template <bool FP8, int WAVES, bool PREFETCH>
+__global__ __launch_bounds__(64 * WAVES) void paged_decode_split_kernel(DecodeParams p) {
+  const int kvh = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  if (kvh >= p.num_kv_heads) return;
+  const int split = blockIdx.y;
+  const int b = blockIdx.z;
+  const int ctx = clamped_len(p, b);
+  const int k_begin = split * p.keys_per_split;
+  const int k_end = min(ctx, k_begin + p.keys_per_split);
+  const bool direct = p.num_splits == 1;
+  if (k_begin >= k_end && !direct) return;  // the merge reads only splits that hold keys
+  decode_segment<FP8, PREFETCH>(p, kvh, b, k_begin, max(k_begin, k_end), direct,
+                                static_cast<int64_t>(b) * p.num_splits + split);
+}
+
+// ---------------------------------------------------------------------------
+// Balanced split-K.  Every sequence is cut into 32-key steps and the steps of
+// all sequences, in sequence order, form one list of T entries (T from a
+// device-side scan of the lengths, so nothing is read back to the host).
+// Range r of the P ranges [r*T/P, (r+1)*T/P) goes to workgroup r, whose WAVES
+// waves are WAVES kv heads; every wave does the same number of steps whatever
+// the length mix.  A range covering a whole sequence writes its output
+// directly; otherwise the piece of sequence b in range r goes to partial slot
+// b + r (distinct for all pieces: ranges and sequences both advance
+// monotonically).  Workgroup (0, 0) also stores the exclusive step prefix of
+// every sequence for the merge.  Grid: (P, head groups).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int shfl_up_i(int v, int d) {
+  const int lane = __lane_id();
+  const int src = lane >= d ? lane - d : lane;
+  return __builtin_amdgcn_ds_bpermute(src << 2, v);
+}
+
+// Inclusive scan over the workgroup (WAVES waves); `total` gets the sum.
+template <int WAVES>
+__device__ __forceinline__ int block_scan_incl(int v, int* s_wsum, int& total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = shfl_up_i(v, d);
+    if (lane >= d) v += t;
+  }
+  if (lane == 63) s_wsum[wave] = v;
+  __syncthreads();
+  int before = 0;
+  total = 0;
+#pragma unroll
+  for (int i = 0; i < WAVES; ++i) {
+    const int s = s_wsum[i];
+    before += i < wave ? s : 0;
+    total += s;
+  }
+  __syncthreads();
+  return v + before;
+}
+
+__device__ __forceinline__ int64_t range_start(int64_t r, int64_t T, int64_t P) { return r * T / P; }
+
+template <bool FP8, int WAVES, bool PREFETCH>
+__global__ __launch_bounds__(64 * WAVES) void paged_decode_balanced_kernel(DecodeParams p) {
+  constexpr int CH = 64 * WAVES;  // sequences per scan chunk
+  __shared__ int s_wsum[WAVES];
+  __shared__ int s_seg[3 * CH];   // (b, first step, end step) of the chunk's pieces
+  const int tid = threadIdx.x;
+  const int kvh = blockIdx.y * WAVES + (tid >> 6);
+  const int r = blockIdx.x;
+  const int B = p.batch;
+  const bool write_prefix = blockIdx.x == 0 && blockIdx.y == 0;
+
+  // pass 1: total step count T (and the prefix array for the merge)
+  int T = 0;
+  for (int c0 = 0; c0 < B; c0 += CH) {
+    const int b = c0 + tid;
+    const int st = b < B ? (clamped_len(p, b) + 31) >> 5 : 0;
+    int tot;
+    const int incl = block_scan_incl<WAVES>(st, s_wsum, tot);
+    if (write_prefix && b < B) p.ws_prefix[b] = T + incl - st;
+    T += tot;
+  }
+  if (write_prefix && tid == 0) p.ws_prefix[B] = T;
+  const int64_t P = p.balanced_ranges;
+  const int start = static_cast<int>(range_start(r, T, P));
+  const int end = static_cast<int>(range_start(r + 1, T, P));
+  if (start >= end) return;  // uniform over the workgroup
+
+  // pass 2: walk the sequences overlapping [start, end), one chunk at a time
+  int carry = 0;
+  for (int c0 = 0; c0 < B && carry < end; c0 += CH) {
+    const int b = c0 + tid;
+    const int st = b < B ? (clamped_len(p, b) + 31) >> 5 : 0;
+    int tot;
+    const int incl = block_scan_incl<WAVES>(st, s_wsum, tot);
+    const int s0 = carry + incl - st;  // first step of sequence b
+    const int s1 = carry + incl;
+    const bool hit = b < B && st > 0 && s0 < end && s1 > start;
+    int nseg;
+    const int pos = block_scan_incl<WAVES>(hit ? 1 : 0, s_wsum, nseg) - 1;
+    if (hit) {
+      s_seg[3 * pos] = b;
+      s_seg[3 * pos + 1] = max(start, s0) - s0;
+      s_seg[3 * pos + 2] = min(end, s1) - s0;
+    }
+    __syncthreads();
+    if (kvh < p.num_kv_heads) {
+      for (int i = 0; i < nseg; ++i) {
+        const int sb = s_seg[3 * i];
+        const int lo = s_seg[3 * i + 1];
+        const int hi = s_seg[3 * i + 2];
+        const int len = clamped_len(p, sb);
+        const bool whole = lo == 0 && hi == ((len + 31) >> 5);
+        decode_segment<FP8, PREFETCH>(p, kvh, sb, 32 * lo, min(32 * hi, len), whole,
+                                      static_cast<int64_t>(sb) + r);
+      }
+    }
+    __syncthreads();  // s_seg is rewritten by the next chunk
+    carry += tot;
+  }
+}
+
+// Log-sum-exp merge of the partials: one wavefront per (sequence, head), two
+// output columns per lane.  Fixed splits: slots b*num_splits + s for the splits
+// that hold keys.  Balanced: slots b + r for the ranges r that overlap the
+// sequence; a sequence inside one range was written directly and is skipped,
+// an empty one gets zeros.
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
   const int bh = blockIdx.x;
   const int b = bh / p.num_heads;
+  const int h = bh - b * p.num_heads;
   const int lane = threadIdx.x;
-  int ctx = p.seqlens[b];
-  const int cap = p.max_blocks * p.block_size;
-  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
-  const int nvalid = (ctx + p.keys_per_split - 1) / p.keys_per_split;
-  const float* ml = p.ws_ml + static_cast<int64_t>(bh) * p.num_splits * 2;
-  const float* wo = p.ws_o + static_cast<int64_t>(bh) * p.num_splits * kHeadDim + 2 * lane;
+  int64_t first, count;
+  bool zero = false;
+  if (p.balanced_ranges > 0) {
+    const int64_t s0 = p.ws_prefix[b], s1 = p.ws_prefix[b + 1], T = p.ws_prefix[p.batch];
+    const int64_t P = p.balanced_ranges;
+    if (s1 <= s0) {
+      zero = true;
+      first = count = 0;
+    } else {
+      const int64_t rf = ((s0 + 1) * P - 1) / T;  // range holding step s0
+      const int64_t rl = (s1 * P - 1) / T;        // range holding step s1 - 1
+      if (rf == rl) return;
+      first = b + rf;
+      count = rl - rf + 1;
+    }
+  } else {
+    const int ctx = clamped_len(p, b);
+    first = static_cast<int64_t>(b) * p.num_splits;
+    count = (ctx + p.keys_per_split - 1) / p.keys_per_split;
+    zero = count == 0;
+  }
   float M = kNegInf;
-  for (int s = 0; s < nvalid; ++s) M = fmaxf(M, ml[2 * s]);
+  for (int64_t s = 0; s < count; ++s) {
+    if (p.balanced_ranges > 0) {  // ranges that are empty (P > T) wrote nothing
+      const int64_t rr = first - b + s;
+      const int64_t T = p.ws_prefix[p.batch];
+      if (range_start(rr, T, p.balanced_ranges) == range_start(rr + 1, T, p.balanced_ranges)) continue;
+    }
+    M = fmaxf(M, p.ws_ml[((first + s) * p.num_heads + h) * 2]);
+  }
   float L = 0.f, o0 = 0.f, o1 = 0.f;
-  if (M != kNegInf) {
-    for (int s = 0; s < nvalid; ++s) {
-      const float w = fast_exp2(ml[2 * s] - M);
-      L += w * ml[2 * s + 1];
-      const f32x2 v = *reinterpret_cast<const f32x2*>(wo + static_cast<int64_t>(s) * kHeadDim);
+  if (!zero && M != kNegInf) {
+    for (int64_t s = 0; s < count; ++s) {
+      if (p.balanced_ranges > 0) {
+        const int64_t rr = first - b + s;
+        const int64_t T = p.ws_prefix[p.batch];
+        if (range_start(rr, T, p.balanced_ranges) == range_start(rr + 1, T, p.balanced_ranges)) continue;
+      }
+      const int64_t idx = (first + s) * p.num_heads + h;
+      const float w = fast_exp2(p.ws_ml[idx * 2] - M);
+      L += w * p.ws_ml[idx * 2 + 1];
+      const f32x2 v = *reinterpret_cast<const f32x2*>(p.ws_o + idx * kHeadDim + 2 * lane);
       o0 += w * v[0];
       o1 += w * v[1];
     }
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  const int h = bh - b * p.num_heads;
   uint32_t* orow = reinterpret_cast<uint32_t*>(p.out + b * p.out_row_stride + h * kHeadDim + 2 * lane);
   *orow = pack_bf16x2(o0 * inv, o1 * inv);
 }
 
+// Launch shape per cache dtype, chosen by measurement on MI355X (config 3 /
+// config 5 shapes): waves per workgroup (kv heads sharing a key range), whether
+// the next step's loads are issued before the current step's math, and the
+// total number of waves the balanced mode spreads the steps over.
+//   bf16: 4 waves, prefetch (256 VGPRs, one wave per SIMD), 1024 waves
+//   fp8 : 8 waves, no prefetch (half the bytes per step), 2048 waves
+template <bool FP8>
+struct DecodeShape;
+template <>
+struct DecodeShape<false> {
+  static constexpr int kWaves = 4;
+  static constexpr bool kPrefetch = true;
+  static constexpr int kTargetWaves = 1024;
+};
+template <>
+struct DecodeShape<true> {
+  static constexpr int kWaves = 8;
+  static constexpr bool kPrefetch = false;
+  static constexpr int kTargetWaves = 2048;
+};
+
+int decode_waves_per_group(int32_t num_kv_heads, int32_t kv_dtype) {
+  int w = kv_dtype == 1 ? DecodeShape<true>::kWaves : DecodeShape<false>::kWaves;
+  while (w > 1 && w / 2 >= num_kv_heads) w /= 2;
+  return w;
+}
+
 DecodePlan plan_decode(int32_t batch, int32_t num_kv_heads, int32_t max_blocks, int32_t block_size,
                        int32_t kv_dtype, int32_t requested_splits) {
-  (void)block_size;
-  (void)kv_dtype;
-  DecodePlan plan;
-  int32_t pps = 1;
-  if (requested_splits > 0) {
-    pps = (max_blocks + requested_splits - 1) / requested_splits;
-  } else {
-    // Widest split that still leaves >= 8192 work items (about 32 per CU):
-    // fewer partials to merge without starving the 256 CUs.
-    const int64_t pairs = static_cast<int64_t>(batch) * num_kv_heads;
-    while (pps < max_blocks) {
-      const int64_t next = 2 * pps;
-      const int64_t items = pairs * ((max_blocks + next - 1) / next);
-      if (items < 8192) break;
-      pps = static_cast<int32_t>(next);
-    }
+  DecodePlan plan{};
+  if (requested_splits > 0) {  // fixed: about requested_splits splits per sequence
+    int32_t pps = (max_blocks + requested_splits - 1) / requested_splits;
+    if (pps < 1) pps = 1;
+    plan.pages_per_split = pps;
+    plan.num_splits = (max_blocks + pps - 1) / pps;
+    plan.balanced_ranges = 0;
+    plan.partial_slots = plan.num_splits > 1 ? static_cast<int64_t>(batch) * plan.num_splits : 0;
+    return plan;
   }
-  if (pps < 1) pps = 1;
-  if (pps > max_blocks) pps = max_blocks > 0 ? max_blocks : 1;
-  plan.pages_per_split = pps;
-  plan.num_splits = max_blocks > 0 ? (max_blocks + pps - 1) / pps : 1;
+  // balanced: about kTargetWaves waves in total, never more ranges than there
+  // can be steps
+  const int w = decode_waves_per_group(num_kv_heads, kv_dtype);
+  const int64_t groups = (num_kv_heads + w - 1) / w;
+  const int target = kv_dtype == 1 ? DecodeShape<true>::kTargetWaves : DecodeShape<false>::kTargetWaves;
+  int64_t P = target / (w * groups);
+  const int64_t max_steps = static_cast<int64_t>(batch) * ((static_cast<int64_t>(max_blocks) * block_size + 31) / 32);
+  if (max_steps >= (int64_t{1} << 31)) return plan_decode(batch, num_kv_heads, max_blocks, block_size, kv_dtype, 1);
+  if (P > max_steps) P = max_steps;
+  if (P < 1) P = 1;
+  plan.pages_per_split = max_blocks;
+  plan.num_splits = 1;
+  plan.balanced_ranges = static_cast<int32_t>(P);
+  plan.partial_slots = batch + P;
   return plan;
+}
+
+template <bool FP8>
+static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
+  constexpr bool PF = DecodeShape<FP8>::kPrefetch;
+  const int w = decode_waves_per_group(p.num_kv_heads, FP8 ? 1 : 0);
+  const unsigned groups = static_cast<unsigned>((p.num_kv_heads + w - 1) / w);
+  constexpr int WMAX = DecodeShape<FP8>::kWaves;  // wider shapes are never launched for this dtype
+#define NVA_LAUNCH_W(KERNEL, GRID)                                                                      \
+  if (w >= 8 && WMAX >= 8)                                                                              \
+    hipLaunchKernelGGL((KERNEL<FP8, (WMAX >= 8 ? 8 : 1), PF>), GRID, dim3(64 * (WMAX >= 8 ? 8 : 1)), 0, \
+                       stream, p);                                                                      \
+  else if (w >= 4)                                                                                      \
+    hipLaunchKernelGGL((KERNEL<FP8, 4, PF>), GRID, dim3(256), 0, stream, p);                            \
+  else if (w >= 2)                                                                                      \
+    hipLaunchKernelGGL((KERNEL<FP8, 2, PF>), GRID, dim3(128), 0, stream, p);                            \
+  else                                                                                                  \
+    hipLaunchKernelGGL((KERNEL<FP8, 1, PF>), GRID, dim3(64), 0, stream, p);
+  bool merge;
+  if (p.balanced_ranges > 0) {
+    const dim3 grid(static_cast<unsigned>(p.balanced_ranges), groups);
+    NVA_LAUNCH_W(paged_decode_balanced_kernel, grid);
+    merge = true;
+  } else {
+    const dim3 grid(groups, p.num_splits, p.batch);
+    NVA_LAUNCH_W(paged_decode_split_kernel, grid);
+    merge = p.num_splits > 1;
+  }
+#undef NVA_LAUNCH_W
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !merge) return e;
+  const dim3 mgrid(static_cast<unsigned>(p.batch * p.num_heads));
+  hipLaunchKernelGGL(decode_merge_kernel, mgrid, dim3(64), 0, stream, p);
+  return hipGetLastError();
 }
 
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, hipStream_t stream) {
   if (p.batch <= 0) return hipSuccess;
-  const dim3 grid(p.num_splits, p.num_kv_heads, p.batch);
-  if (kv_dtype == 1)
-    hipLaunchKernelGGL(paged_decode_kernel<true>, grid, dim3(64), 0, stream, p);
-  else
-    hipLaunchKernelGGL(paged_decode_kernel<false>, grid, dim3(64), 0, stream, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.num_splits == 1) return e;
-  const dim3 mgrid(static_cast<unsigned>(p.batch * p.num_heads));
-  hipLaunchKernelGGL(decode_merge_kernel, mgrid, dim3(64), 0, stream, p);
-  return hipGetLastError();
+  return kv_dtype == 1 ? launch_decode_t<true>(p, stream) : launch_decode_t<false>(p, stream);
 }
 
 }  // namespace nva

@@ -142,14 +142,21 @@ def test_decode_rejects(lib, kw, code):
 
 def test_decode_workspace_plan(lib):
     f = lib.nva_decode_workspace_bytes
-    # one split -> no workspace
-    assert f(4, 16, 8, 128, 1, 256, 0, 0) == 0
+    rnd = lambda x: (x + 255) // 256 * 256
+    # fixed mode, one split: no workspace
+    assert f(4, 16, 8, 128, 1, 256, 0, 1) == 0
     assert f(256, 16, 8, 128, 8, 256, 0, 1) == 0
-    # explicit split count: ceil(8 / 2) = 4 pages per split -> 2 splits
-    assert f(256, 16, 8, 128, 8, 256, 0, 2) == 256 * 16 * 2 * (128 + 2) * 4
-    # heuristic: deterministic, depends only on sizes
-    a = f(256, 16, 8, 128, 8, 256, 0, 0)
-    assert a == f(256, 16, 8, 128, 8, 256, 0, 0) and a > 0
+    # fixed mode: ceil(8 / 2) = 4 pages per split -> 2 splits per sequence
+    assert f(256, 16, 8, 128, 8, 256, 0, 2) == rnd(256 * 2 * 16 * (128 + 2) * 4)
+    # balanced mode (num_splits = 0): B + P slots plus the step prefix, where
+    # P ranges of 4 kv-head waves (two head groups) make about 1024 bf16 waves
+    assert f(256, 16, 8, 128, 8, 256, 0, 0) == rnd((256 + 128) * 16 * 130 * 4 + 257 * 4)
+    # fp8: ranges of 8 kv-head waves, about 2048 waves
+    assert f(64, 64, 8, 128, 128, 256, 1, 0) == rnd((64 + 256) * 64 * 130 * 4 + 65 * 4)
+    # never more ranges than steps: 2 sequences x 1 page x 8 steps
+    assert f(2, 16, 8, 128, 1, 256, 0, 0) == rnd((2 + 16) * 16 * 130 * 4 + 3 * 4)
+    # deterministic, and nothing for an empty batch
+    assert f(64, 64, 8, 128, 128, 256, 1, 0) == f(64, 64, 8, 128, 128, 256, 1, 0) > 0
     assert f(0, 16, 8, 128, 8, 256, 0, 0) == 0
 
 

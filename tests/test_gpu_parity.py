@@ -186,6 +186,40 @@ def test_decode_group_sizes(dev, nh, nkv, fp8):
         assert_attn_close(got, decode_reference(case), what=f"nh={nh} nkv={nkv} fp8={fp8} splits={ns}", **tol)
 
 
+@pytest.mark.parametrize("lengths,width", [
+    ([5, 0, 3000, 1, 0, 64, 4097, 33], 17),   # zero-length rows mixed in, long rows spanning ranges
+    ([1] * 9, 1),                              # more ranges than steps
+    ([700] * 3 + [0] * 5, 3),
+])
+@pytest.mark.parametrize("fp8", [False, True])
+def test_decode_balanced_partition(dev, lengths, width, fp8):
+    """Balanced split-K (num_splits=0) against the oracle and against fixed splits."""
+    from nanovllm_amd import workloads as W
+    case = W.make_decode_case(len(lengths), 32, 8, 0, 0, 64, fp8=fp8, seed=len(lengths) + width,
+                              bulk_device=dev, lengths=lengths, table_width=width)
+    bal = _run_decode(case, 0, store=False)
+    tol = dict(max_abs=FP8_MAX_ABS, mean_abs=FP8_MAX_ABS) if fp8 else {}
+    assert_attn_close(bal, decode_reference(case), what=f"balanced {lengths}", **tol)
+    for ns in (1, 3):
+        fixed = _run_decode(case, ns, store=False)
+        assert np.abs(fixed - bal).max() <= 1e-2
+    for b, L in enumerate(lengths):
+        if L == 0:
+            assert np.all(bal[b] == 0)
+
+
+def test_decode_balanced_many_sequences(dev):
+    """Batch above one scan chunk (512 sequences) with short, uneven contexts."""
+    from nanovllm_amd import workloads as W
+    g = torch.Generator().manual_seed(5)
+    lengths = torch.randint(0, 300, (1300,), generator=g).tolist()
+    case = W.make_decode_case(1300, 16, 8, 0, 0, 1700, seed=8, bulk_device=dev, lengths=lengths, table_width=2)
+    got = _run_decode(case, 0, store=False)
+    seqs = list(range(0, 1300, 37))
+    assert_attn_close(got[seqs], decode_reference(case, seqs), what="1300 sequences")
+    assert np.all(got[[b for b, L in enumerate(lengths) if L == 0]] == 0)
+
+
 def test_decode_zero_and_single_key(dev):
     from nanovllm_amd import workloads as W
     lengths = [0, 1, 5, 0]
