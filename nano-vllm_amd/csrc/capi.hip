@@ -131,6 +131,16 @@ int nva_prefill(const void* q, int64_t q_row_stride, const void* k, int64_t k_ro
       (k_row_stride % 8) || (v_row_stride % 8) || (out_row_stride % 8))
     return fail(NVA_ERR_UNSUPPORTED, "q/k/v/out must be 16-byte aligned with row strides a multiple of 8 elements");
   if (!(softmax_scale > 0.f)) return fail(NVA_ERR_INVALID_ARGUMENT, "softmax_scale must be positive");
+  if (num_heads / num_kv_heads > nva::kPrefillMaxGroup)
+    return fail(NVA_ERR_UNSUPPORTED, "GQA group %d above %d not supported", num_heads / num_kv_heads,
+                nva::kPrefillMaxGroup);
+  {
+    const int bp = nva::prefill_positions_per_tile(num_heads / num_kv_heads);
+    if ((static_cast<int64_t>(max_seqlen_q) + bp - 1) / bp > 65535)
+      return fail(NVA_ERR_UNSUPPORTED, "max_seqlen_q %d too long for the launch grid", max_seqlen_q);
+    if (static_cast<int64_t>(num_seqs) * num_kv_heads > 0x7fffffffLL)
+      return fail(NVA_ERR_UNSUPPORTED, "num_seqs*num_kv_heads above 2^31-1");
+  }
   if (block_table) {
     if (block_size <= 0 || block_size % 64 != 0)
       return fail(NVA_ERR_UNSUPPORTED, "paged prefill needs block_size a positive multiple of 64 (got %d)", block_size);

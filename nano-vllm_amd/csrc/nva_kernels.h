@@ -72,13 +72,16 @@ struct PrefillParams {
   int32_t num_heads;
   int32_t num_kv_heads;
   int32_t group;
-  int32_t num_q_tiles;        // ceil(max_seqlen_q * group / rows per workgroup)
+  int32_t num_q_tiles;        // ceil(max_seqlen_q / positions_per_tile)
+  int32_t positions_per_tile; // query positions per workgroup (x group = rows)
   float scale_log2;
 };
 
 hipError_t launch_store_kvcache(const StoreParams& p, int vec_bytes, hipStream_t stream);
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, hipStream_t stream);
 hipError_t launch_prefill(const PrefillParams& p, int max_seqlen_q, hipStream_t stream);
+int prefill_positions_per_tile(int group);  // query positions one prefill workgroup covers
+constexpr int kPrefillMaxGroup = 256;        // rows per prefill workgroup bound the GQA group
 
 // Split-K plan shared by nva_decode and nva_decode_workspace_bytes.
 // balanced_ranges > 0: balanced mode with that many step ranges; otherwise
