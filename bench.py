@@ -34,6 +34,18 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def profiled_traffic(key: str):
+    """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (scaled by a
+    plain copy of known size), as recorded in the committed profile summary."""
+    path = ROOT / "profiles" / "decode_hbm_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith(f"traffic_bytes_per_launch {key}"):
+            return int(float(line.split(":")[1].split()[0]))
+    return None
+
+
 def _pools(case, n):
     """n independent (k_cache, v_cache) pools with identical contents."""
     pools = [(case.k_cache, case.v_cache)]
@@ -219,9 +231,11 @@ def main(argv=None):
         line["config"] = {"workload": "config 3: decode step = store_kvcache(new token) + paged GQA decode",
                           "batch": 256, "context": "U[100,2048]", "num_heads": 16, "num_kv_heads": 8,
                           "head_dim": 128, "block_size": 256, "pool_pages": 2048, "cache_pools_rotated": 2}
-        line["roofline"] = {"kernel": "paged decode (paged_decode_kernel + decode_merge_kernel)",
+        line["roofline"] = {"kernel": "paged decode (paged_decode_balanced_kernel + decode_merge_kernel)",
                             "bound": "hbm", "achieved": round(d3["attn_gbs"], 1), "peak": HBM_PEAK_GBS,
-                            "unit": "GB/s", "frac": round(d3["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                            "unit": "GB/s", "frac": round(d3["attn_gbs"] / HBM_PEAK_GBS, 4),
+                            "traffic": profiled_traffic("config3"),
+                            "traffic_source": "profiles/decode_hbm_traffic.md",
                             "bytes_per_launch": d3["attn_bytes"], "launch_us": round(d3["attn_ms"] * 1e3, 2)}
         line["store_kvcache_us"] = round(d3["store_ms"] * 1e3, 2)
     if "cpu" in out:
@@ -234,7 +248,8 @@ def main(argv=None):
     if "cfg5" in out:
         d5 = out["cfg5"]
         line["fp8_decode"] = {"cfg5": {"gbs": round(d5["attn_gbs"], 1), "frac": round(d5["attn_gbs"] / HBM_PEAK_GBS, 4),
-                                       "attn_us": round(d5["attn_ms"] * 1e3, 2), "bytes": d5["attn_bytes"]}}
+                                       "attn_us": round(d5["attn_ms"] * 1e3, 2), "bytes": d5["attn_bytes"],
+                                       "traffic": profiled_traffic("config5")}}
     if "value" not in line:
         k = next(iter(out))
         line["value"] = None

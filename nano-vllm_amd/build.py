@@ -44,9 +44,18 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
+# Per-file extras.  The prefill kernel's softmax never relies on NaN
+# propagation (masked scores are -inf, not NaN), so max() can skip the
+# IEEE quieting of its operands.
+FILE_FLAGS = {
+    "varlen_prefill.hip": ["-fno-honor-nans"],
+}
+
+
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *HIP_FLAGS, f"-I{CSRC}", f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), f"-I{CSRC}", f"-I{INCLUDE}", "-c", str(src),
+           "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -62,6 +62,19 @@ __device__ __forceinline__ float shfl_xor(float v, int mask) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src << 2, __builtin_bit_cast(int, v)));
 }
 
+// Max over lanes l, l^16, l^32, l^48 (the four lane groups holding one MFMA
+// column) with gfx950 row swaps: called with the same value as both operands,
+// v_permlane16_swap / v_permlane32_swap return {x[l], x[l^16]} /
+// {x[l], x[l^32]} in some order, so combining the pair is order-free.
+__device__ __forceinline__ float max_across_groups(float v) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  v = fmaxf(__builtin_bit_cast(float, r16[0]), __builtin_bit_cast(float, r16[1]));
+  const uint32_t c = __builtin_bit_cast(uint32_t, v);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+  return fmaxf(__builtin_bit_cast(float, r32[0]), __builtin_bit_cast(float, r32[1]));
+}
+
 // v_perm_b32: selector byte k picks byte (sel_k) of the 8-byte value {hi:a, lo:b}.
 __device__ __forceinline__ uint32_t perm(uint32_t a, uint32_t b, uint32_t sel) {
   return __builtin_amdgcn_perm(a, b, sel);

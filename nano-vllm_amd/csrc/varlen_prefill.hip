@@ -20,7 +20,10 @@
 // rate covers the K/V operand reads this costs.  Key tile rows are ordered so
 // that the S^T accumulator of lane l holds row (l % 16)'s scores for keys
 // 8*(l/16) .. +7 -- the P^T operand layout of O^T += V^T . P^T -- so the
-// probabilities never leave the lane.  Softmax runs online in the exp2 domain
+// probabilities never leave the lane.  The row sums of the probabilities come
+// from the matrix pipe as well (one extra MFMA against an all-ones operand per
+// column tile), so they use the same bf16 weights as the numerator and cost no
+// VALU adds.  Softmax runs online in the exp2 domain
 // with a lazily updated row maximum: the maximum used for the exponent moves
 // only when a new score exceeds it by more than kTau (so p <= 2^kTau), which
 // makes the rescale of the 32 accumulator registers per tile rare.  Masks are
@@ -172,12 +175,14 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[nt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[kNT], l_run[kNT];
+  float m_run[kNT];
+  f32x4 lacc[kNT];  // row sums of the probabilities (every element of the 4 holds the sum)
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt) {
     m_run[nt] = kNegInf;
-    l_run[nt] = 0.f;
+    lacc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  const bf16x8 ones = as_bf16x8(u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
   const float sl2 = p.scale_log2;
 
   const int krow0 = 8 * (n >> 2) + (n & 3);
@@ -250,34 +255,28 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
         }
         float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                          fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
-        mx *= sl2;  // log2 domain (sl2 > 0)
+        mx = max_across_groups(mx) * sl2;  // log2 domain (sl2 > 0)
         // lazy maximum: move it only when a score exceeds it by more than kTau
         const bool grow = mx > m_run[nt] + kTau;
         if (__builtin_amdgcn_ballot_w64(grow)) {
           const float m_new = grow ? mx : m_run[nt];
           const float alpha = fast_exp2(m_run[nt] - m_new);  // 1 for lanes that keep their maximum
-          l_run[nt] *= alpha;
+          lacc[nt] *= alpha;
 #pragma unroll
           for (int j = 0; j < 8; ++j) acc[nt][j] *= alpha;
           m_run[nt] = m_new;
         }
         const float m_use = m_run[nt] == kNegInf ? 0.f : m_run[nt];
         float pv[8];
-        float psum = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          pv[i] = fast_exp2(__builtin_fmaf(sv[i], sl2, -m_use));
-          psum += pv[i];
-        }
-        l_run[nt] += psum;
+        for (int i = 0; i < 8; ++i) pv[i] = fast_exp2(__builtin_fmaf(sv[i], sl2, -m_use));
         u32x4 pw;
 #pragma unroll
         for (int q2 = 0; q2 < 4; ++q2) pw[q2] = pack_bf16x2(pv[2 * q2], pv[2 * q2 + 1]);
         const bf16x8 pop = as_bf16x8(pw);
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[nt][j] = mfma16x16x32(vt[j], pop, acc[nt][j]);
+        lacc[nt] = mfma16x16x32(ones, pop, lacc[nt]);
       }
     }
     if (more) store_tile(pre, sK[buf ^ 1], sVt[buf ^ 1], tid);
@@ -287,9 +286,7 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   // ---- epilogue: normalise and write rows ------------------------------------
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt) {
-    float l = l_run[nt];
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
+    const float l = lacc[nt][0];
     if (pos[nt] < 0) continue;
     const int r = kRowsPerWave * w + 16 * nt + n;
     const int h = kvh * G + r % G;
