@@ -127,6 +127,8 @@ int nva_prefill(const void* q, int64_t q_row_stride, const void* k, int64_t k_ro
     return fail(NVA_ERR_INVALID_ARGUMENT, "q/out row strides must be >= num_heads*head_dim");
   if (k_row_stride < kd || v_row_stride < kd)
     return fail(NVA_ERR_INVALID_ARGUMENT, "k/v row strides must be >= num_kv_heads*head_dim");
+  if (k_row_stride > (int64_t{1} << 24) || v_row_stride > (int64_t{1} << 24))
+    return fail(NVA_ERR_UNSUPPORTED, "k/v row strides above 2^24 elements not supported");
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16) || (q_row_stride % 8) ||
       (k_row_stride % 8) || (v_row_stride % 8) || (out_row_stride % 8))
     return fail(NVA_ERR_UNSUPPORTED, "q/k/v/out must be 16-byte aligned with row strides a multiple of 8 elements");

@@ -13,6 +13,7 @@ namespace nva {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -28,6 +29,35 @@ __device__ __forceinline__ u32x4 as_u32x4(bf16x8 v) { return __builtin_bit_cast(
 // Lane l receives C rows 4*(l/16) + r, r = 0..3, of column (l % 16).
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// D = A(32x16) * B(16x32) + C.  Lane l supplies A row (l % 32) and B column
+// (l % 32) with 8 contraction elements owned by lane half (l / 32); lane l
+// receives C rows 8*(i/4) + 4*(l/32) + i%4, i = 0..15, of column (l % 32).
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// v_permlane32_swap: swaps the upper 32 lanes of `a` with the lower 32 lanes
+// of `b`, so with a = b = x the pair holds x[l & 31] and x[l | 32], i.e. lanes
+// l and l^32 in some order.  Inline asm because this compiler's builtin loses
+// the second result (the optimiser replaces it by the first).  The s_nop
+// gives the wait states a VALU write of an operand needs before the swap.
+__device__ __forceinline__ void permlane32_swap(uint32_t& a, uint32_t& b) {
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+// Max / sum over lanes l and l^32 (the two halves holding one 32x32 MFMA column).
+__device__ __forceinline__ float max_across_halves(float v) {
+  uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+  permlane32_swap(a, b);
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
+__device__ __forceinline__ float sum_across_halves(float v) {
+  uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+  permlane32_swap(a, b);
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
 }
 
 // 16-byte and 8-byte global loads / stores through plain vector memory ops.
@@ -60,19 +90,6 @@ __device__ __forceinline__ float shfl_xor(float v, int mask) {
   int lane = __lane_id();
   int src = lane ^ mask;
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src << 2, __builtin_bit_cast(int, v)));
-}
-
-// Max over lanes l, l^16, l^32, l^48 (the four lane groups holding one MFMA
-// column) with gfx950 row swaps: called with the same value as both operands,
-// v_permlane16_swap / v_permlane32_swap return {x[l], x[l^16]} /
-// {x[l], x[l^32]} in some order, so combining the pair is order-free.
-__device__ __forceinline__ float max_across_groups(float v) {
-  const uint32_t b = __builtin_bit_cast(uint32_t, v);
-  const auto r16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
-  v = fmaxf(__builtin_bit_cast(float, r16[0]), __builtin_bit_cast(float, r16[1]));
-  const uint32_t c = __builtin_bit_cast(uint32_t, v);
-  const auto r32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
-  return fmaxf(__builtin_bit_cast(float, r32[0]), __builtin_bit_cast(float, r32[1]));
 }
 
 // v_perm_b32: selector byte k picks byte (sel_k) of the 8-byte value {hi:a, lo:b}.

@@ -9,33 +9,29 @@
 // therefore share every K/V tile the workgroup stages.  Keys are visited in
 // 64-key tiles, triple-buffered in LDS and filled by global->LDS DMA
 // (global_load_lds_dwordx4: no registers, no VALU):
-//   K [64 keys][256 B]  16-byte pieces XOR-swizzled by key row
-//   V [64 keys][256 B]  32-byte chunks XOR-swizzled by key row
+//   K [64 keys][256 B]  16-byte pieces XOR-swizzled by key row (row & 15)
+//   V [64 keys][256 B]  32-byte chunks XOR-swizzled by key row (2 * (row & 3))
 // Each lane of a DMA instruction lands 16 B at LDS base + 16 * lane, so the
 // swizzles are made by choosing every lane's source address.  The DMA of tile
 // i+2 is issued before the math of tile i, so a tile has two tiles of math to
-// arrive (one barrier per tile).  The
-// V^T MFMA operand (8 consecutive keys of one dim per lane) is read with
-// gfx950's transposing LDS read ds_read_b64_tr_b16: within a 16-lane group,
-// lane i receives element i % 4 of the 8 bytes addressed by lanes
-// 4e + i / 4 (e = 0..3), so when lane j addresses key row base + j / 4 at dims
-// 4 (j % 4) .. +3, lane i holds dim i of keys base .. base + 3.
+// arrive (one barrier per tile).
 //
-// Per 32-key step a wave computes S^T = K . Q^T (keys x rows) for its two
-// 16-row column tiles with 16x16x32 bf16 MFMAs.  32 rows per wave keep Q, the
-// O accumulators, the K/V operands and the staging registers within 256 VGPRs
-// (two waves per SIMD, no accumulator traffic to AGPRs); gfx950's LDS read
-// rate covers the K/V operand reads this costs.  Key tile rows are ordered so
-// that the S^T accumulator of lane l holds row (l % 16)'s scores for keys
-// 8*(l/16) .. +7 -- the P^T operand layout of O^T += V^T . P^T -- so the
-// probabilities never leave the lane.  The row sums of the probabilities come
-// from the matrix pipe as well (one extra MFMA against an all-ones operand per
-// column tile), so they use the same bf16 weights as the numerator and cost no
-// VALU adds.  Softmax runs online in the exp2 domain
-// with a lazily updated row maximum: the maximum used for the exponent moves
-// only when a new score exceeds it by more than kTau (so p <= 2^kTau), which
-// makes the rescale of the 32 accumulator registers per tile rare.  Masks are
-// evaluated only on tiles that cross the causal diagonal or the key end.
+// Per 32-key step a wave computes the 32 keys x 32 rows tile S^T = K . Q^T with
+// 32x32x16 bf16 MFMAs (two accumulation chains over the head dim).  Lane l owns
+// row l % 32 and keys 8b + 4h + r (h = l / 32, b, r = 0..3) of the step, so
+// the row maximum needs one permlane32 swap, and the probabilities of
+// registers 8u .. 8u+7 are exactly the P^T operand of PV MFMA u (keys
+// 16u + 8(e/4) + 4h + e%4) -- they never leave the lane.  The matching V^T
+// operand (those 8 keys of one head dim per lane) is read with gfx950's
+// transposing LDS read ds_read_b64_tr_b16: within a 16-lane group, lane i
+// receives element i % 4 of the 8 bytes addressed by lanes 4e + i / 4, so
+// when lane j addresses key row base + j / 4 at dims 4 (j % 4) .. +3, lane i
+// holds dim i of keys base .. base + 3.
+//
+// Softmax runs online in the exp2 domain with a lazily updated row maximum: it
+// moves only when a score exceeds it by more than kTau (so p <= 2^kTau), which
+// makes the rescale of the accumulators rare.  Masks are evaluated only on
+// tiles that cross the causal diagonal or the key end.
 #include "nva_common.h"
 #include "nva_kernels.h"
 
@@ -45,19 +41,18 @@ namespace {
 
 constexpr int kWaves = 8;
 constexpr int kRowsPerWave = 32;
-constexpr int kNT = kRowsPerWave / 16;      // MFMA column tiles per wave
 constexpr int kRows = kWaves * kRowsPerWave;  // (position, head) rows per workgroup
-constexpr int kBK = 64;                     // keys per LDS tile
+constexpr int kBK = 64;                       // keys per LDS tile
 constexpr float kNegInf = -__builtin_huge_valf();
-constexpr float kTau = 8.0f;                // lazy-rescale threshold (log2 units)
+constexpr float kTau = 8.0f;                  // lazy-rescale threshold (log2 units)
+constexpr float kInitMax = -1e30f;            // finite: exp2(fma(s, c, -m)) never sees -inf - -inf
 
-// Swizzle of the 16-byte piece index inside a K row: the 16 rows one MFMA
-// operand read touches map to 16 distinct bank groups.
-__device__ __forceinline__ int k_swz(int row) { return (row & 3) | (((row >> 3) & 3) << 2); }
-// Swizzle of the 32-byte chunk index inside a V row: the 16 rows (4 per lane
-// group) of one transposing read map to 8 chunk positions, two rows each --
-// the minimum of two passes for a 512-byte read.
-__device__ __forceinline__ int v_swz(int row) { return (row & 3) | (((row >> 3) & 1) << 2); }
+// K: 16-byte piece swizzle; the 16 consecutive rows one quarter-wave of an
+// operand read touches land in 16 distinct bank groups.
+__device__ __forceinline__ int k_swz(int row) { return row & 15; }
+// V: 32-byte chunk swizzle; each half-wave of a transposing read (4 rows x 2
+// chunks) lands in 8 distinct 32-byte bank groups.
+__device__ __forceinline__ int v_swz(int row) { return 2 * (row & 3); }
 
 constexpr int kTileBytes = kBK * kHeadDim * 2;  // one K (or V) tile: 16 KiB
 constexpr int kStageBytes = 2 * kTileBytes;      // K + V
@@ -70,8 +65,17 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // All but the last tile's four DMA instructions have completed.
 __device__ __forceinline__ void wait_vmem_keep4() { asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); }
+// Workgroup barrier that drains this wave's LDS reads but not its in-flight
+// global->LDS DMA (the release fence of __syncthreads would wait for both).
+__device__ __forceinline__ void barrier_keep_dma() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-constexpr float kInitMax = -1e30f;  // finite: exp2(fma(s, c, -m)) never sees -inf - -inf
+__device__ __forceinline__ bf16x8 read_tr_pair(const char* p0, const char* p1) {
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p1);
+  const u32x2 a = __builtin_bit_cast(u32x2, lo);
+  const u32x2 b = __builtin_bit_cast(u32x2, hi);
+  return as_bf16x8(u32x4{a[0], a[1], b[0], b[1]});
+}
 
 }  // namespace
 
@@ -81,9 +85,10 @@ constexpr float kInitMax = -1e30f;  // finite: exp2(fma(s, c, -m)) never sees -i
 struct DmaLane {
   int row[4];
   int col[4];
+  uint32_t off[4];  // byte offset of (row, col) from the tile's first key
 };
 
-__device__ __forceinline__ DmaLane dma_lane(int w, int lane) {
+__device__ __forceinline__ DmaLane dma_lane(int w, int lane, int64_t stride) {
   DmaLane d;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -94,16 +99,22 @@ __device__ __forceinline__ DmaLane dma_lane(int w, int lane) {
     d.row[u] = row;
     d.col[u] = off < kTileBytes ? (piece ^ k_swz(row)) * 8
                                 : ((piece >> 1) ^ v_swz(row)) * 16 + (piece & 1) * 8;
+    d.off[u] = static_cast<uint32_t>((row * stride + d.col[u]) * 2);
   }
   return d;
 }
 
+typedef const __attribute__((address_space(4))) int32_t const_i32;
+
 // DMA of one 64-key K/V tile into LDS stage `st` (32 KiB).  Keys at or beyond
 // kmax are redirected to the tile's first key, a valid row whose scores the
 // masks remove; a block id outside the pool redirects the tile to slot 0.
+// The block table is read through the constant address space (a scalar load,
+// counted by lgkmcnt): a vector load would be counted by vmcnt, and waiting
+// for it would also wait for the K/V DMA still in flight.
 template <bool PAGED>
 __device__ __forceinline__ void dma_tile(char* st, const PrefillParams& p, const uint16_t* base, int64_t stride,
-                                         const DmaLane& d, const int32_t* bt, int k_start, int kb, int kmax,
+                                         const DmaLane& d, const_i32* bt, int k_start, int kb, int kmax,
                                          int w) {
   int64_t slot0;
   if constexpr (PAGED) {
@@ -114,13 +125,12 @@ __device__ __forceinline__ void dma_tile(char* st, const PrefillParams& p, const
   } else {
     slot0 = static_cast<int64_t>(k_start) + kb;
   }
-  const uint16_t* tile = base + slot0 * stride;
+  const char* tile = reinterpret_cast<const char*>(base + slot0 * stride);
   const int nrow = kmax - kb;  // rows that exist (>= 64 except in the last tile)
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int row = d.row[u] < nrow ? d.row[u] : 0;
-    const uint16_t* src = tile + row * stride + d.col[u];
-    __builtin_amdgcn_global_load_lds((gvoid*)src, (lvoid*)(st + (4 * w + u) * 1024), 16, 0, 0);
+    const uint32_t off = d.row[u] < nrow ? d.off[u] : static_cast<uint32_t>(d.col[u] * 2);
+    __builtin_amdgcn_global_load_lds((gvoid*)(tile + off), (lvoid*)(st + (4 * w + u) * 1024), 16, 0, 0);
   }
 }
 
@@ -148,25 +158,23 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   const int tid = threadIdx.x;
   const int w = tid >> 6;
   const int lane = tid & 63;
-  const int n = lane & 15;
-  const int g = lane >> 4;
+  const int n = lane & 31;  // row of this lane within the wave's 32
+  const int h = lane >> 5;  // lane half
   const int nrows = BP * G;
 
-  // rows of this lane: r = 32w + 16nt + n
-  int pos[kNT];
-  bf16x8 qop[kNT][4];
+  // Q^T operand: row r = 32w + n, head dims 16 ks + 8h .. +7 for MFMA step ks.
+  const int r = kRowsPerWave * w + n;
+  const int qp = i0 + r / G;
+  const int qh = kvh * G + r % G;
+  const bool row_ok = r < nrows && qp < Lq;
+  const int pos = row_ok ? qp : -1;
+  bf16x8 qop[8];
+  {
+    const uint16_t* qrow = p.q + static_cast<int64_t>(q_start + qp) * p.q_row_stride + qh * kHeadDim + 8 * h;
 #pragma unroll
-  for (int nt = 0; nt < kNT; ++nt) {
-    const int r = kRowsPerWave * w + 16 * nt + n;
-    const int qp = i0 + r / G;
-    const int h = kvh * G + r % G;
-    const bool ok = r < nrows && qp < Lq;
-    pos[nt] = ok ? qp : -1;
-    const uint16_t* qrow = p.q + static_cast<int64_t>(q_start + qp) * p.q_row_stride + h * kHeadDim;
-#pragma unroll
-    for (int sidx = 0; sidx < 4; ++sidx) {
+    for (int ks = 0; ks < 8; ++ks) {
       const u32x4 z = {0u, 0u, 0u, 0u};
-      qop[nt][sidx] = as_bf16x8(ok ? ld16(qrow + 32 * sidx + 8 * g) : z);
+      qop[ks] = as_bf16x8(row_ok ? ld16(qrow + 16 * ks) : z);
     }
   }
 
@@ -179,40 +187,35 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   const int wpos_hi = w_last >= w_first ? min(i0 + w_last / G, Lq - 1) : wpos_lo - 1;
   const int wave_kmax = wpos_hi >= wpos_lo ? max(0, min(kmax, wpos_hi + off + 1)) : 0;
   const int wave_full = wpos_lo + off + 1;  // keys below this are visible to every row of the wave
+  const int limit = pos < 0 ? -1 : min(pos + off, kmax - 1);  // last key this row sees
 
-  f32x4 acc[kNT][8];
+  f32x16 acc[4];  // O^T, head dims 32 jd + 8 b + 4 h + r of row n
 #pragma unroll
-  for (int nt = 0; nt < kNT; ++nt)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[nt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[kNT];
-  f32x4 lacc[kNT];  // row sums of the probabilities (every element of the 4 holds the sum)
-#pragma unroll
-  for (int nt = 0; nt < kNT; ++nt) {
-    m_run[nt] = kInitMax;
-    lacc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  const bf16x8 ones = as_bf16x8(u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+  for (int jd = 0; jd < 4; ++jd) acc[jd] = f32x16{};
+  float m_run = kInitMax;
+  float l_run = 0.f;  // this lane's half of the row sum
   const float sl2 = p.scale_log2;
 
-  // Per-lane LDS byte offsets of the MFMA operand reads inside a stage; the key
-  // tile (t), the 32-key half (sub) and the 4-key half (hh) add constants.
-  //   K: row krow0 + 4t + 32sub, piece (4 sidx + g) ^ k_swz(row) = (4 sidx + g) ^ n
-  //   V: row 8g + 4hh + n/4 + 32sub, chunk j ^ v_swz(row) = j ^ (n/4 | (g&1) << 2)
-  const int krow0 = 8 * (n >> 2) + (n & 3);
-  int kaddr[4];
+  // Per-lane LDS byte offsets of the MFMA operand reads inside a stage; the
+  // 32-key half (sub), PV MFMA (u) and 4-key block (eb) add constants.
+  //   K: row n + 32 sub, piece (2 ks + h) ^ (row & 15)
+  //   V: row 16u + 8eb + 4h + j/4 + 32 sub (j = lane % 16),
+  //      chunk (2 jd + (lane/16 & 1)) ^ 2 (j/4), byte 8 (j % 4)
+  int kaddr[8];
 #pragma unroll
-  for (int sidx = 0; sidx < 4; ++sidx) kaddr[sidx] = krow0 * 256 + ((4 * sidx + g) ^ n) * 16;
-  const int vs = (n >> 2) | ((g & 1) << 2);
-  int vaddr[8];
+  for (int ks = 0; ks < 8; ++ks) kaddr[ks] = n * 256 + ((2 * ks + h) ^ (n & 15)) * 16;
+  const int jl = lane & 15;
+  int vaddr[4];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) vaddr[j] = kTileBytes + (8 * g + (n >> 2)) * 256 + 8 * (n & 3) + (j ^ vs) * 32;
+  for (int jd = 0; jd < 4; ++jd)
+    vaddr[jd] = kTileBytes + (4 * h + (jl >> 2)) * 256 + ((2 * jd + ((lane >> 4) & 1)) ^ (2 * (jl >> 2))) * 32 +
+                8 * (jl & 3);
 
-  const DmaLane dl = dma_lane(w, lane);
   const bool k_wave = w < 4;  // waves 0..3 stage K, 4..7 stage V
-  const int32_t* bt = PAGED ? p.block_table + s * p.bt_row_stride : nullptr;
+  const_i32* bt = PAGED ? (const_i32*)(p.block_table + s * p.bt_row_stride) : nullptr;
   const uint16_t* dbase = (k_wave ? p.k : p.v) + kvh * kHeadDim;
   const int64_t dstride = k_wave ? p.k_row_stride : p.v_row_stride;
+  const DmaLane dl = dma_lane(w, lane, dstride);
   const int ntiles = (kmax + kBK - 1) / kBK;
 
   // One 64-key tile: start the DMA of tile it+2 into `nxt`, run the math on
@@ -227,79 +230,72 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
       if (key0 < wave_kmax) {  // otherwise every key of this step is masked for this wave
         const bool need_mask = key0 + 32 > wave_full || key0 + 32 > kmax;
         const char* sb = cur + 8192 * sub;
-        bf16x8 kop[2][4];
+        // S^T = K . Q^T over the 128 head dims: two chains of four MFMAs
+        f32x16 s0 = f32x16{}, s1 = f32x16{};
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int sidx = 0; sidx < 4; ++sidx)
-            kop[t][sidx] = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + kaddr[sidx] + 1024 * t));
-        // V^T operands: dims 16j .. 16j+15 of keys 8g .. 8g+7 (two transposing reads)
-        bf16x8 vt[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(sb + vaddr[j]));
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(sb + vaddr[j] + 1024));
-          const u32x2 a = __builtin_bit_cast(u32x2, lo);
-          const u32x2 b = __builtin_bit_cast(u32x2, hi);
-          vt[j] = as_bf16x8(u32x4{a[0], a[1], b[0], b[1]});
+        for (int ks = 0; ks < 8; ks += 2) {
+          const bf16x8 k0 = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + kaddr[ks]));
+          const bf16x8 k1 = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + kaddr[ks + 1]));
+          s0 = mfma32x32x16(k0, qop[ks], s0);
+          s1 = mfma32x32x16(k1, qop[ks + 1], s1);
         }
-        // Column tiles one after another, software-pipelined by one tile: the
-        // QK^T MFMAs of tile nt+1 are issued before the softmax of tile nt, so the
-        // VALU work overlaps the matrix pipe while only two score sets are live.
-        f32x4 st[2][2];
-        auto qk = [&](f32x4 (&d)[2], int nt) {
+        // V^T operands: head dims 32 jd .. +31 of PV MFMA u's 16 keys
+        bf16x8 vt[4][2];
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            d[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int jd = 0; jd < 4; ++jd)
 #pragma unroll
-            for (int sidx = 0; sidx < 4; ++sidx) d[t] = mfma16x16x32(kop[t][sidx], qop[nt][sidx], d[t]);
+          for (int u = 0; u < 2; ++u)
+            vt[jd][u] = read_tr_pair(sb + vaddr[jd] + 4096 * u, sb + vaddr[jd] + 4096 * u + 2048);
+        float sv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sv[i] = s0[i] + s1[i];
+        if (need_mask) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = key0 + 8 * (i >> 2) + 4 * h + (i & 3);
+            sv[i] = key <= limit ? sv[i] : kNegInf;
           }
-        };
-        qk(st[0], 0);
+        }
+        float mx = sv[0];
 #pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) {
-          const int curb = nt & 1;
-          if (nt + 1 < kNT) qk(st[curb ^ 1], nt + 1);
-          float sv[8];
+        for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sv[i]);
+        mx = max_across_halves(mx) * sl2;  // log2 domain (sl2 > 0)
+        // lazy maximum: move it only when a score exceeds it by more than kTau
+        const bool grow = mx > m_run + kTau;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+          const float m_new = grow ? mx : m_run;
+          const float alpha = fast_exp2(m_run - m_new);  // 1 for lanes that keep their maximum
+          l_run *= alpha;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) sv[i] = st[curb][i >> 2][i & 3];
-          if (need_mask) {
-            const int limit = pos[nt] < 0 ? -1 : min(pos[nt] + off, kmax - 1);  // last visible key
+          for (int jd = 0; jd < 4; ++jd) acc[jd] *= alpha;
+          m_run = m_new;
+        }
+        const float mneg = -m_run;
+        float pv[16];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) sv[i] = (key0 + 8 * g + i <= limit) ? sv[i] : kNegInf;
-          }
-          float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                           fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-          mx = max_across_groups(mx) * sl2;  // log2 domain (sl2 > 0)
-          // lazy maximum: move it only when a score exceeds it by more than kTau
-          const bool grow = mx > m_run[nt] + kTau;
-          if (__builtin_amdgcn_ballot_w64(grow)) {
-            const float m_new = grow ? mx : m_run[nt];
-            const float alpha = fast_exp2(m_run[nt] - m_new);  // 1 for lanes that keep their maximum
-            lacc[nt] *= alpha;
+        for (int i = 0; i < 16; ++i) {
+          pv[i] = fast_exp2(__builtin_fmaf(sv[i], sl2, mneg));
+          l_run += pv[i];
+        }
+        bf16x8 pop[2];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[nt][j] *= alpha;
-            m_run[nt] = m_new;
-          }
-          const float mneg = -m_run[nt];
-          float pv[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) pv[i] = fast_exp2(__builtin_fmaf(sv[i], sl2, mneg));
+        for (int u = 0; u < 2; ++u) {
           u32x4 pw;
 #pragma unroll
-          for (int q2 = 0; q2 < 4; ++q2) pw[q2] = pack_bf16x2(pv[2 * q2], pv[2 * q2 + 1]);
-          const bf16x8 pop = as_bf16x8(pw);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[nt][j] = mfma16x16x32(vt[j], pop, acc[nt][j]);
-          lacc[nt] = mfma16x16x32(ones, pop, lacc[nt]);
+          for (int q2 = 0; q2 < 4; ++q2) pw[q2] = pack_bf16x2(pv[8 * u + 2 * q2], pv[8 * u + 2 * q2 + 1]);
+          pop[u] = as_bf16x8(pw);
         }
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int jd = 0; jd < 4; ++jd) acc[jd] = mfma32x32x16(vt[jd][u], pop[u], acc[jd]);
       }
     }
     if (issue)
       wait_vmem_keep4();  // tile it+1 has landed; tile it+2 may still be in flight ...
     else
       wait_vmem_all();
-    __syncthreads();  // ... for every wave; stage `cur` is free again
+    barrier_keep_dma();  // ... for every wave; stage `cur` is free again
   };
 
   if (ntiles > 0) dma_tile<PAGED>(smem0, p, dbase, dstride, dl, bt, k_start, 0, kmax, w);
@@ -309,30 +305,27 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   } else {
     wait_vmem_all();
   }
-  __syncthreads();
+  barrier_keep_dma();
   for (int it = 0; it < ntiles; it += 3) {
     tile_step(it, smem0, smem2);
     if (it + 1 < ntiles) tile_step(it + 1, smem1, smem0);
     if (it + 2 < ntiles) tile_step(it + 2, smem2, smem1);
   }
 
-  // ---- epilogue: normalise and write rows ------------------------------------
+  // ---- epilogue: normalise and write the row ----------------------------------
+  const float l = sum_across_halves(l_run);
+  if (pos < 0) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  uint16_t* orow = p.out + static_cast<int64_t>(q_start + pos) * p.out_row_stride + qh * kHeadDim + 4 * h;
 #pragma unroll
-  for (int nt = 0; nt < kNT; ++nt) {
-    const float l = lacc[nt][0];
-    if (pos[nt] < 0) continue;
-    const int r = kRowsPerWave * w + 16 * nt + n;
-    const int h = kvh * G + r % G;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    uint16_t* orow = p.out + static_cast<int64_t>(q_start + pos[nt]) * p.out_row_stride + h * kHeadDim + 4 * g;
+  for (int jd = 0; jd < 4; ++jd)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int b = 0; b < 4; ++b) {
       u32x2 o;
-      o[0] = pack_bf16x2(acc[nt][j][0] * inv, acc[nt][j][1] * inv);
-      o[1] = pack_bf16x2(acc[nt][j][2] * inv, acc[nt][j][3] * inv);
-      *reinterpret_cast<u32x2*>(orow + 16 * j) = o;
+      o[0] = pack_bf16x2(acc[jd][4 * b] * inv, acc[jd][4 * b + 1] * inv);
+      o[1] = pack_bf16x2(acc[jd][4 * b + 2] * inv, acc[jd][4 * b + 3] * inv);
+      *reinterpret_cast<u32x2*>(orow + 32 * jd + 8 * b) = o;
     }
-  }
 }
 
 int prefill_positions_per_tile(int group) { return group >= 1 && group <= kRows ? kRows / group : 1; }

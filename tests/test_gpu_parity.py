@@ -326,6 +326,40 @@ def test_prefill_prefix_shapes(dev, prefix, shared):
     assert_attn_close(got, prefill_reference(case), what=f"prefix={prefix} shared={shared}")
 
 
+SPIKE_POSITIONS = (5, 37, 70, 100, 131, 250)  # spread over both lane halves and several steps
+
+
+@pytest.mark.parametrize("prefix", [0, 256])
+def test_prefill_score_outliers(dev, prefix):
+    """A few keys score ~160 log2 units above the rest.  A row maximum that
+    misses any lane holding part of the row lets exp2 overflow to inf."""
+    from nanovllm_amd import workloads as W
+    lens = [200, 77, 300]
+    case = W.make_prefill_case(lens, 16, 8, 24, prefix_len=prefix, seed=91 + prefix, bulk_device=dev,
+                               shared_prefix=False)
+    case.q.fill_(1.0)  # score of a key = scale * sum of its entries
+    cu = case.cu_seqlens_q.cpu().tolist()
+    for s, L in enumerate(lens):
+        for p in SPIKE_POSITIONS:
+            if p < L:
+                case.k[cu[s] + p] = 10.0  # scale * 1280 = 113 nats
+    got = _run_prefill(case)
+    assert_attn_close(got, prefill_reference(case), what=f"outliers prefix={prefix}")
+
+
+def test_decode_score_outliers(dev):
+    from nanovllm_amd import workloads as W
+    case = W.make_decode_case(6, 16, 8, 300, 900, 24, seed=93, bulk_device=dev)
+    case.q.fill_(1.0)
+    bt = case.block_tables.cpu()
+    for b in range(case.batch):
+        for p in SPIKE_POSITIONS + (299,):
+            page = int(bt[b, p // case.block_size])
+            case.k_cache[page, p % case.block_size] = 10.0
+    got = _run_decode(case)
+    assert_attn_close(got, decode_reference(case), what="decode outliers")
+
+
 def test_prefill_prefix_equals_full_tail(dev):
     """Prefix-cached prefill == the last Lq rows of a full prefill over prefix+suffix."""
     from nanovllm_amd import workloads as W
