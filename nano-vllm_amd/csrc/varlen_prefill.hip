@@ -7,17 +7,19 @@
 // row is one (query position, query head) pair of the kv head's GQA group
 // (rows are position-major: row r = position r / G, head r % G).  All G heads
 // therefore share every K/V tile the workgroup stages.  Keys are visited in
-// 64-key tiles, triple-buffered in LDS and filled by global->LDS DMA
-// (global_load_lds_dwordx4: no registers, no VALU):
+// 64-key tiles held in a 4-stage LDS ring:
 //   K [64 keys][256 B]  16-byte pieces XOR-swizzled by key row (row & 15)
 //   V [64 keys][256 B]  32-byte chunks XOR-swizzled by key row (2 * (row & 3))
-// Each lane of a DMA instruction lands 16 B at LDS base + 16 * lane, so the
-// swizzles are made by choosing every lane's source address.  The DMA of tile
-// i+2 is issued before the math of tile i, so a tile has two tiles of math to
-// arrive (one barrier per tile).
+// Every lane stages 16-byte pieces: it loads them from global memory into
+// registers one tile ahead and writes them to LDS at 16 * lane inside its
+// wave's KiB, so the swizzles are made by choosing each lane's source address.
+// (Global->LDS DMA, global_load_lds_dwordx4, measured slower here.)  One
+// barrier per tile, placed between the tile's two 32-key steps.
 //
 // Per 32-key step a wave computes the 32 keys x 32 rows tile S^T = K . Q^T with
-// 32x32x16 bf16 MFMAs (two accumulation chains over the head dim).  Lane l owns
+// 32x32x16 bf16 MFMAs (two accumulation chains over the head dim), and the
+// MFMAs of the next step's S^T are issued between the exponentials of the
+// current one, so the matrix pipe and the VALU overlap.  Lane l owns
 // row l % 32 and keys 8b + 4h + r (h = l / 32, b, r = 0..3) of the step, so
 // the row maximum needs one permlane32 swap, and the probabilities of
 // registers 8u .. 8u+7 are exactly the P^T operand of PV MFMA u (keys
@@ -56,18 +58,15 @@ __device__ __forceinline__ int v_swz(int row) { return 2 * (row & 3); }
 
 constexpr int kTileBytes = kBK * kHeadDim * 2;  // one K (or V) tile: 16 KiB
 constexpr int kStageBytes = 2 * kTileBytes;      // K + V
+constexpr int kStages = 4;                        // LDS ring depth (128 KiB)
 
-typedef __attribute__((address_space(1))) void gvoid;
-typedef __attribute__((address_space(3))) void lvoid;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-__device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-// All but the last tile's four DMA instructions have completed.
-__device__ __forceinline__ void wait_vmem_keep4() { asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); }
-// Workgroup barrier that drains this wave's LDS reads but not its in-flight
-// global->LDS DMA (the release fence of __syncthreads would wait for both).
-__device__ __forceinline__ void barrier_keep_dma() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// Workgroup barrier after this wave's LDS accesses have completed.  Unlike
+// __syncthreads it does not also wait for the global loads still in flight
+// (the tile staged in registers one tile ahead).
+__device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ bf16x8 read_tr_pair(const char* p0, const char* p1) {
   const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
@@ -79,17 +78,17 @@ __device__ __forceinline__ bf16x8 read_tr_pair(const char* p0, const char* p1) {
 
 }  // namespace
 
-// Per-lane constants of the DMA that fills a stage: every wave issues four
-// 1 KiB instructions; lane `lane` of instruction u fills key row `row[u]`,
-// element offset `col[u]` inside that row (K for waves 0..3, V for 4..7).
-struct DmaLane {
+// Per-lane constants of the staging of a tile: every wave moves four 1 KiB
+// pieces; lane `lane` of piece u carries key row `row[u]`, element offset
+// `col[u]` inside that row (K for waves 0..3, V for 4..7).
+struct StageLane {
   int row[4];
   int col[4];
   uint32_t off[4];  // byte offset of (row, col) from the tile's first key
 };
 
-__device__ __forceinline__ DmaLane dma_lane(int w, int lane, int64_t stride) {
-  DmaLane d;
+__device__ __forceinline__ StageLane stage_lane(int w, int lane, int64_t stride) {
+  StageLane d;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int off = (4 * w + u) * 1024;
@@ -106,16 +105,16 @@ __device__ __forceinline__ DmaLane dma_lane(int w, int lane, int64_t stride) {
 
 typedef const __attribute__((address_space(4))) int32_t const_i32;
 
-// DMA of one 64-key K/V tile into LDS stage `st` (32 KiB).  Keys at or beyond
-// kmax are redirected to the tile's first key, a valid row whose scores the
-// masks remove; a block id outside the pool redirects the tile to slot 0.
-// The block table is read through the constant address space (a scalar load,
-// counted by lgkmcnt): a vector load would be counted by vmcnt, and waiting
-// for it would also wait for the K/V DMA still in flight.
+// Global loads of this wave's quarter-KiB pieces of one 64-key K/V tile into
+// registers (`r`); store_tile later writes them to their swizzled LDS places.
+// Keys at or beyond kmax are redirected to the tile's first key, a valid row
+// whose scores the masks remove; a block id outside the pool redirects the
+// tile to slot 0.  The block table is read through the constant address
+// space (a scalar load, counted by lgkmcnt, not vmcnt).
 template <bool PAGED>
-__device__ __forceinline__ void dma_tile(char* st, const PrefillParams& p, const uint16_t* base, int64_t stride,
-                                         const DmaLane& d, const_i32* bt, int k_start, int kb, int kmax,
-                                         int w) {
+__device__ __forceinline__ void load_tile(u32x4 (&r)[4], const PrefillParams& p, const uint16_t* base,
+                                          int64_t stride, const StageLane& d, const_i32* bt, int k_start, int kb,
+                                          int kmax) {
   int64_t slot0;
   if constexpr (PAGED) {
     const int bi = kb / p.block_size;
@@ -130,17 +129,25 @@ __device__ __forceinline__ void dma_tile(char* st, const PrefillParams& p, const
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const uint32_t off = d.row[u] < nrow ? d.off[u] : static_cast<uint32_t>(d.col[u] * 2);
-    __builtin_amdgcn_global_load_lds((gvoid*)(tile + off), (lvoid*)(st + (4 * w + u) * 1024), 16, 0, 0);
+    r[u] = ld16(tile + off);
   }
+}
+
+// Lane `lane` of wave `w` owns bytes (4w + u) KiB + 16 lane of the stage.
+__device__ __forceinline__ void store_tile(char* st, const u32x4 (&r)[4], int w, int lane) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) st16(st + (4 * w + u) * 1024 + 16 * lane, r[u]);
 }
 
 template <bool PAGED>
 __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillParams p) {
-  // Three stages as separate objects, so the compiler can prove that reads of
-  // one stage never alias the DMA filling another and need not wait for it.
+  // Four stages as separate objects, so the compiler can prove that reads of
+  // one stage never alias the writes filling another.
   __shared__ __attribute__((aligned(1024))) char smem0[kStageBytes];
   __shared__ __attribute__((aligned(1024))) char smem1[kStageBytes];
   __shared__ __attribute__((aligned(1024))) char smem2[kStageBytes];
+  __shared__ __attribute__((aligned(1024))) char smem3[kStageBytes];
+  char* const smem[kStages] = {smem0, smem1, smem2, smem3};
 
   const int s = blockIdx.x / p.num_kv_heads;
   const int kvh = blockIdx.x - s * p.num_kv_heads;
@@ -215,101 +222,112 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   const_i32* bt = PAGED ? (const_i32*)(p.block_table + s * p.bt_row_stride) : nullptr;
   const uint16_t* dbase = (k_wave ? p.k : p.v) + kvh * kHeadDim;
   const int64_t dstride = k_wave ? p.k_row_stride : p.v_row_stride;
-  const DmaLane dl = dma_lane(w, lane, dstride);
+  const StageLane dl = stage_lane(w, lane, dstride);
   const int ntiles = (kmax + kBK - 1) / kBK;
 
-  // One 64-key tile: start the DMA of tile it+2 into `nxt`, run the math on
-  // `cur`, wait for tile it+1 and synchronise.
-  auto tile_step = [&](int it, const char* cur, char* nxt) {
-    const int kb = it * kBK;
-    const bool issue = it + 2 < ntiles;
-    if (issue) dma_tile<PAGED>(nxt, p, dbase, dstride, dl, bt, k_start, kb + 2 * kBK, kmax, w);
+  // S^T = K . Q^T for the 32 keys at `sb`, as two partial sums (two MFMA
+  // chains over the head dims) that the consumer adds.
+  auto qk = [&](const char* sb, f32x16& s0, f32x16& s1) {
+    bf16x8 kr[8];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int key0 = kb + 32 * sub;
-      if (key0 < wave_kmax) {  // otherwise every key of this step is masked for this wave
-        const bool need_mask = key0 + 32 > wave_full || key0 + 32 > kmax;
-        const char* sb = cur + 8192 * sub;
-        // S^T = K . Q^T over the 128 head dims: two chains of four MFMAs
-        f32x16 s0 = f32x16{}, s1 = f32x16{};
+    for (int ks = 0; ks < 8; ++ks) kr[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + kaddr[ks]));
+    s0 = f32x16{};
+    s1 = f32x16{};
 #pragma unroll
-        for (int ks = 0; ks < 8; ks += 2) {
-          const bf16x8 k0 = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + kaddr[ks]));
-          const bf16x8 k1 = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + kaddr[ks + 1]));
-          s0 = mfma32x32x16(k0, qop[ks], s0);
-          s1 = mfma32x32x16(k1, qop[ks + 1], s1);
-        }
-        // V^T operands: head dims 32 jd .. +31 of PV MFMA u's 16 keys
-        bf16x8 vt[4][2];
-#pragma unroll
-        for (int jd = 0; jd < 4; ++jd)
-#pragma unroll
-          for (int u = 0; u < 2; ++u)
-            vt[jd][u] = read_tr_pair(sb + vaddr[jd] + 4096 * u, sb + vaddr[jd] + 4096 * u + 2048);
-        float sv[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sv[i] = s0[i] + s1[i];
-        if (need_mask) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = key0 + 8 * (i >> 2) + 4 * h + (i & 3);
-            sv[i] = key <= limit ? sv[i] : kNegInf;
-          }
-        }
-        float mx = sv[0];
-#pragma unroll
-        for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sv[i]);
-        mx = max_across_halves(mx) * sl2;  // log2 domain (sl2 > 0)
-        // lazy maximum: move it only when a score exceeds it by more than kTau
-        const bool grow = mx > m_run + kTau;
-        if (__builtin_amdgcn_ballot_w64(grow)) {
-          const float m_new = grow ? mx : m_run;
-          const float alpha = fast_exp2(m_run - m_new);  // 1 for lanes that keep their maximum
-          l_run *= alpha;
-#pragma unroll
-          for (int jd = 0; jd < 4; ++jd) acc[jd] *= alpha;
-          m_run = m_new;
-        }
-        const float mneg = -m_run;
-        float pv[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          pv[i] = fast_exp2(__builtin_fmaf(sv[i], sl2, mneg));
-          l_run += pv[i];
-        }
-        bf16x8 pop[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          u32x4 pw;
-#pragma unroll
-          for (int q2 = 0; q2 < 4; ++q2) pw[q2] = pack_bf16x2(pv[8 * u + 2 * q2], pv[8 * u + 2 * q2 + 1]);
-          pop[u] = as_bf16x8(pw);
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-          for (int jd = 0; jd < 4; ++jd) acc[jd] = mfma32x32x16(vt[jd][u], pop[u], acc[jd]);
-      }
+    for (int ks = 0; ks < 8; ks += 2) {
+      s0 = mfma32x32x16(kr[ks], qop[ks], s0);
+      s1 = mfma32x32x16(kr[ks + 1], qop[ks + 1], s1);
     }
-    if (issue)
-      wait_vmem_keep4();  // tile it+1 has landed; tile it+2 may still be in flight ...
-    else
-      wait_vmem_all();
-    barrier_keep_dma();  // ... for every wave; stage `cur` is free again
   };
 
-  if (ntiles > 0) dma_tile<PAGED>(smem0, p, dbase, dstride, dl, bt, k_start, 0, kmax, w);
-  if (ntiles > 1) {
-    dma_tile<PAGED>(smem1, p, dbase, dstride, dl, bt, k_start, kBK, kmax, w);
-    wait_vmem_keep4();
-  } else {
-    wait_vmem_all();
-  }
-  barrier_keep_dma();
-  for (int it = 0; it < ntiles; it += 3) {
-    tile_step(it, smem0, smem2);
-    if (it + 1 < ntiles) tile_step(it + 1, smem1, smem0);
-    if (it + 2 < ntiles) tile_step(it + 2, smem2, smem1);
+  // One 32-key step: softmax of the scores sa + sb of keys key0 .. key0+31
+  // and O^T += V^T P^T with V from `sb_v`; the QK MFMAs of the following step
+  // (keys at `sb_next`) are issued in between, so the matrix pipe works on
+  // them while the VALU does the exponentials.  Without a following step they
+  // run on `sb_v` and their result is unused, which keeps the block branch-free.
+  auto step = [&](f32x16& sa, f32x16& sb, int key0, const char* sb_v, const char* sb_next, bool next) {
+    if (key0 < wave_kmax) {  // otherwise every key of this step is masked for this wave
+      float sv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sv[i] = sa[i] + sb[i];
+      if (key0 + 32 > wave_full || key0 + 32 > kmax) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = key0 + 8 * (i >> 2) + 4 * h + (i & 3);
+          sv[i] = key <= limit ? sv[i] : kNegInf;
+        }
+      }
+      float mx = sv[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sv[i]);
+      mx = max_across_halves(mx) * sl2;  // log2 domain (sl2 > 0)
+      // lazy maximum: move it only when a score exceeds it by more than kTau
+      const bool grow = mx > m_run + kTau;
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float m_new = grow ? mx : m_run;
+        const float alpha = fast_exp2(m_run - m_new);  // 1 for lanes that keep their maximum
+        l_run *= alpha;
+#pragma unroll
+        for (int jd = 0; jd < 4; ++jd) acc[jd] *= alpha;
+        m_run = m_new;
+      }
+      qk(next ? sb_next : sb_v, sa, sb);
+      const float mneg = -m_run;
+      float pv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        pv[i] = fast_exp2(__builtin_fmaf(sv[i], sl2, mneg));
+        l_run += pv[i];
+      }
+      bf16x8 pop[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        u32x4 pw;
+#pragma unroll
+        for (int q2 = 0; q2 < 4; ++q2) pw[q2] = pack_bf16x2(pv[8 * u + 2 * q2], pv[8 * u + 2 * q2 + 1]);
+        pop[u] = as_bf16x8(pw);
+      }
+      // V^T operands: head dims 32 jd .. +31 of PV MFMA u's 16 keys
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int jd = 0; jd < 4; ++jd) {
+          const bf16x8 vt = read_tr_pair(sb_v + vaddr[jd] + 4096 * u, sb_v + vaddr[jd] + 4096 * u + 2048);
+          acc[jd] = mfma32x32x16(vt, pop[u], acc[jd]);
+        }
+    }
+  };
+
+  // Tile `it` (in stage `cur`, tile it+1 in `nxt`): step over its first 32
+  // keys; synchronise, after which every wave is done with tile it-1 and
+  // tile it+1 is visible; write tile it+2 (loaded one tile ago) into the stage
+  // `fill` that tile it-2 left, and load tile it+3; then step over the last
+  // 32 keys while the QK of tile it+1's first step issues.
+  f32x16 sa = f32x16{}, sb = f32x16{};
+  u32x4 stg[4];  // this wave's share of the tile in flight
+  auto tile_iter = [&](int it, const char* cur, const char* nxt, char* fill) {
+    const int kb = it * kBK;
+    step(sa, sb, kb, cur, cur + 8192, true);
+    barrier_lds();
+    if (it > 0 && it + 2 < ntiles) store_tile(fill, stg, w, lane);
+    if (it + 3 < ntiles) load_tile<PAGED>(stg, p, dbase, dstride, dl, bt, k_start, kb + 3 * kBK, kmax);
+    step(sa, sb, kb + 32, cur + 8192, nxt, it + 1 < ntiles);
+  };
+
+  // prologue: tiles 0 .. 2 in LDS, the first QK issued
+#pragma unroll
+  for (int t = 0; t < kStages - 1; ++t)
+    if (t < ntiles) {
+      load_tile<PAGED>(stg, p, dbase, dstride, dl, bt, k_start, t * kBK, kmax);
+      store_tile(smem[t], stg, w, lane);
+    }
+  barrier_lds();
+  if (0 < wave_kmax) qk(smem0, sa, sb);
+  for (int it = 0; it < ntiles; it += kStages) {
+    tile_iter(it, smem0, smem1, smem2);
+    if (it + 1 < ntiles) tile_iter(it + 1, smem1, smem2, smem3);
+    if (it + 2 < ntiles) tile_iter(it + 2, smem2, smem3, smem0);
+    if (it + 3 < ntiles) tile_iter(it + 3, smem3, smem0, smem1);
   }
 
   // ---- epilogue: normalise and write the row ----------------------------------
