@@ -11,7 +11,7 @@
 //   K [64 keys][256 B]  16-byte pieces XOR-swizzled by key row (row & 15)
 //   V [64 keys][256 B]  32-byte chunks XOR-swizzled by key row (2 * (row & 3))
 // Every lane stages 16-byte pieces: it loads them from global memory into
-// registers one tile ahead and writes them to LDS at 16 * lane inside its
+// registers two tiles ahead and writes them to LDS at 16 * lane inside its
 // wave's KiB, so the swizzles are made by choosing each lane's source address.
 // (Global->LDS DMA, global_load_lds_dwordx4, measured slower here.)  One
 // barrier per tile, placed between the tile's two 32-key steps.
@@ -300,34 +300,41 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
 
   // Tile `it` (in stage `cur`, tile it+1 in `nxt`): step over its first 32
   // keys; synchronise, after which every wave is done with tile it-1 and
-  // tile it+1 is visible; write tile it+2 (loaded one tile ago) into the stage
-  // `fill` that tile it-2 left, and load tile it+3; then step over the last
-  // 32 keys while the QK of tile it+1's first step issues.
+  // tile it+1 is visible; write tile it+2 (loaded two tiles ago, in `set`)
+  // into the stage `fill` that tile it-2 left, and load tile it+4 into `set`;
+  // then step over the last 32 keys while the QK of tile it+1's first step
+  // issues.  Global loads thus have two tiles of math to arrive.
   f32x16 sa = f32x16{}, sb = f32x16{};
-  u32x4 stg[4];  // this wave's share of the tile in flight
-  auto tile_iter = [&](int it, const char* cur, const char* nxt, char* fill) {
+  u32x4 stg[2][4];  // this wave's share of two tiles in flight (tile i+2 in stg[i % 2])
+  auto tile_iter = [&](int it, const char* cur, const char* nxt, char* fill, u32x4 (&set)[4]) {
     const int kb = it * kBK;
     step(sa, sb, kb, cur, cur + 8192, true);
     barrier_lds();
-    if (it > 0 && it + 2 < ntiles) store_tile(fill, stg, w, lane);
-    if (it + 3 < ntiles) load_tile<PAGED>(stg, p, dbase, dstride, dl, bt, k_start, kb + 3 * kBK, kmax);
+    if (it + 2 < ntiles) store_tile(fill, set, w, lane);
+    if (it + 4 < ntiles) load_tile<PAGED>(set, p, dbase, dstride, dl, bt, k_start, kb + 4 * kBK, kmax);
     step(sa, sb, kb + 32, cur + 8192, nxt, it + 1 < ntiles);
   };
 
-  // prologue: tiles 0 .. 2 in LDS, the first QK issued
+  // prologue: tiles 0 and 1 in LDS, tiles 2 and 3 in flight (all loads
+  // issued at once), the first QK issued
+  {
+    u32x4 pro[2][4];
 #pragma unroll
-  for (int t = 0; t < kStages - 1; ++t)
-    if (t < ntiles) {
-      load_tile<PAGED>(stg, p, dbase, dstride, dl, bt, k_start, t * kBK, kmax);
-      store_tile(smem[t], stg, w, lane);
-    }
+    for (int t = 0; t < 2; ++t)
+      if (t < ntiles) load_tile<PAGED>(pro[t], p, dbase, dstride, dl, bt, k_start, t * kBK, kmax);
+    if (2 < ntiles) load_tile<PAGED>(stg[0], p, dbase, dstride, dl, bt, k_start, 2 * kBK, kmax);
+    if (3 < ntiles) load_tile<PAGED>(stg[1], p, dbase, dstride, dl, bt, k_start, 3 * kBK, kmax);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      if (t < ntiles) store_tile(smem[t], pro[t], w, lane);
+  }
   barrier_lds();
   if (0 < wave_kmax) qk(smem0, sa, sb);
   for (int it = 0; it < ntiles; it += kStages) {
-    tile_iter(it, smem0, smem1, smem2);
-    if (it + 1 < ntiles) tile_iter(it + 1, smem1, smem2, smem3);
-    if (it + 2 < ntiles) tile_iter(it + 2, smem2, smem3, smem0);
-    if (it + 3 < ntiles) tile_iter(it + 3, smem3, smem0, smem1);
+    tile_iter(it, smem0, smem1, smem2, stg[0]);
+    if (it + 1 < ntiles) tile_iter(it + 1, smem1, smem2, smem3, stg[1]);
+    if (it + 2 < ntiles) tile_iter(it + 2, smem2, smem3, smem0, stg[0]);
+    if (it + 3 < ntiles) tile_iter(it + 3, smem3, smem0, smem1, stg[1]);
   }
 
   // ---- epilogue: normalise and write the row ----------------------------------
