@@ -141,13 +141,9 @@ __device__ __forceinline__ void store_tile(char* st, const u32x4 (&r)[4], int w,
 
 template <bool PAGED>
 __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillParams p) {
-  // Four stages as separate objects, so the compiler can prove that reads of
-  // one stage never alias the writes filling another.
-  __shared__ __attribute__((aligned(1024))) char smem0[kStageBytes];
-  __shared__ __attribute__((aligned(1024))) char smem1[kStageBytes];
-  __shared__ __attribute__((aligned(1024))) char smem2[kStageBytes];
-  __shared__ __attribute__((aligned(1024))) char smem3[kStageBytes];
-  char* const smem[kStages] = {smem0, smem1, smem2, smem3};
+  // The ring: stage i % 4 holds 64-key tile i.
+  __shared__ __attribute__((aligned(1024))) char smem_all[kStages * kStageBytes];
+  auto stage = [&](int i) { return smem_all + (i & (kStages - 1)) * kStageBytes; };
 
   const int s = blockIdx.x / p.num_kv_heads;
   const int kvh = blockIdx.x - s * p.num_kv_heads;
@@ -326,22 +322,23 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
     if (3 < ntiles) load_tile<PAGED>(stg[1], p, dbase, dstride, dl, bt, k_start, 3 * kBK, kmax);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
-      if (t < ntiles) store_tile(smem[t], pro[t], w, lane);
+      if (t < ntiles) store_tile(stage(t), pro[t], w, lane);
   }
   barrier_lds();
-  if (0 < wave_kmax) qk(smem0, sa, sb);
-  for (int it = 0; it < ntiles; it += kStages) {
-    tile_iter(it, smem0, smem1, smem2, stg[0]);
-    if (it + 1 < ntiles) tile_iter(it + 1, smem1, smem2, smem3, stg[1]);
-    if (it + 2 < ntiles) tile_iter(it + 2, smem2, smem3, smem0, stg[0]);
-    if (it + 3 < ntiles) tile_iter(it + 3, smem3, smem0, smem1, stg[1]);
+  if (0 < wave_kmax) qk(stage(0), sa, sb);
+  for (int it = 0; it < ntiles; it += 2) {
+    tile_iter(it, stage(it), stage(it + 1), stage(it + 2), stg[0]);
+    if (it + 1 < ntiles) tile_iter(it + 1, stage(it + 1), stage(it + 2), stage(it + 3), stg[1]);
   }
 
-  // ---- epilogue: normalise and write the row ----------------------------------
+  // ---- epilogue: normalise, transpose through LDS, write whole rows --------
+  // Each wave owns 8 KiB of the (now idle) ring: row n of its 32 at n * 256 B,
+  // 16-byte chunk c (dims 8c .. 8c+7) at position c ^ (n & 15).  Read back,
+  // 16 consecutive lanes cover one row, so every store writes whole lines.
   const float l = sum_across_halves(l_run);
-  if (pos < 0) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  uint16_t* orow = p.out + static_cast<int64_t>(q_start + pos) * p.out_row_stride + qh * kHeadDim + 4 * h;
+  barrier_lds();  // every wave is done with the ring
+  char* ot = smem_all + w * 8192;
 #pragma unroll
   for (int jd = 0; jd < 4; ++jd)
 #pragma unroll
@@ -349,8 +346,21 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
       u32x2 o;
       o[0] = pack_bf16x2(acc[jd][4 * b] * inv, acc[jd][4 * b + 1] * inv);
       o[1] = pack_bf16x2(acc[jd][4 * b + 2] * inv, acc[jd][4 * b + 3] * inv);
-      *reinterpret_cast<u32x2*>(orow + 32 * jd + 8 * b) = o;
+      const int c = 4 * jd + b;
+      *reinterpret_cast<u32x2*>(ot + n * 256 + ((c ^ (n & 15)) * 16) + 8 * h) = o;
     }
+  const int c = lane & 15;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int rr = 4 * i + (lane >> 4);  // row within the wave
+    const int r2 = 32 * w + rr;
+    const int qp2 = i0 + r2 / G;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ot + rr * 256 + ((c ^ (rr & 15)) * 16));
+    if (r2 < nrows && qp2 < Lq) {
+      uint16_t* dst = p.out + static_cast<int64_t>(q_start + qp2) * p.out_row_stride + (kvh * G + r2 % G) * kHeadDim + 8 * c;
+      st16(dst, v);
+    }
+  }
 }
 
 int prefill_positions_per_tile(int group) { return group >= 1 && group <= kRows ? kRows / group : 1; }
