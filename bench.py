@@ -10,7 +10,8 @@ the 256 MB Infinity Cache cannot serve them.  Alongside: prefill TFLOP/s
 GB/s (config 5), the roofline of the dominant kernel (HIP events on the launch
 stream) and the PyTorch CPU baseline (gather + SDPA) on the host cores.
 
-Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-cpu] [--only decode|prefill|fp8]
+Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--warm-seconds 1] [--no-cpu]
+                       [--only decode|prefill|fp8]
 """
 from __future__ import annotations
 
@@ -46,6 +47,23 @@ def profiled_traffic(key: str):
     return None
 
 
+def _warm(fn, warmup, seconds):
+    """`warmup` untimed calls, then more until `seconds` of wall time have passed:
+    the clocks of an idle MI355X take a while to reach their sustained level, and
+    the timed steps should see that level, not the ramp."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    i = warmup
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
 def _pools(case, n):
     """n independent (k_cache, v_cache) pools with identical contents."""
     pools = [(case.k_cache, case.v_cache)]
@@ -54,7 +72,7 @@ def _pools(case, n):
     return pools
 
 
-def bench_decode(case, steps, warmup, n_pools=2, with_store=True):
+def bench_decode(case, steps, warmup, n_pools=2, with_store=True, warm_s=1.0):
     import torch
     import nanovllm_amd as nva
     pools = _pools(case, n_pools)
@@ -69,11 +87,12 @@ def bench_decode(case, steps, warmup, n_pools=2, with_store=True):
         return nva.flash_attn_with_kvcache(q, kc, vc, case.context_lens, case.block_tables, case.scale,
                                            k_scale=case.k_scale, v_scale=case.v_scale)
 
-    for i in range(warmup):
+    def one(i):
         if with_store:
             store(i)
         attend(i)
-    torch.cuda.synchronize()
+
+    _warm(one, warmup, warm_s)
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -99,7 +118,7 @@ def bench_decode(case, steps, warmup, n_pools=2, with_store=True):
                 attn_gbs=attn_bytes / (attn_ms * 1e-3) / 1e9)
 
 
-def bench_prefill(case, steps, warmup):
+def bench_prefill(case, steps, warmup, warm_s=1.0):
     import torch
     import nanovllm_amd as nva
     nva.store_kvcache(case.k, case.v, case.k_cache, case.v_cache, case.slot_mapping)
@@ -112,9 +131,7 @@ def bench_prefill(case, steps, warmup):
         return nva.flash_attn_varlen_func(case.q, k, v, case.max_seqlen_q, case.cu_seqlens_q, case.max_seqlen_k,
                                           case.cu_seqlens_k, case.scale, True, case.block_tables)
 
-    for _ in range(warmup):
-        run()
-    torch.cuda.synchronize()
+    _warm(lambda i: run(), warmup, warm_s)
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
     for i in range(steps):
         ev[i][0].record()
@@ -163,6 +180,8 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warm-seconds", type=float, default=1.0,
+                    help="after the warmup steps, keep running each workload untimed for this long")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["decode", "prefill", "fp8"], default=None)
     ap.add_argument("--copy-probe", action="store_true",
@@ -191,7 +210,7 @@ def main(argv=None):
     if args.only in (None, "decode"):
         log("[bench] config 3: decode step (store + paged decode), B=256")
         c3 = W.config3(dev)
-        d3 = bench_decode(c3, steps, warmup)
+        d3 = bench_decode(c3, steps, warmup, warm_s=args.warm_seconds)
         log(f"[bench] cfg3 step {d3['step_ms']*1e3:.1f} us, attention {d3['attn_ms']*1e3:.1f} us "
             f"= {d3['attn_gbs']:.0f} GB/s, store {d3['store_ms']*1e3:.1f} us")
         out["cfg3"] = d3
@@ -204,19 +223,19 @@ def main(argv=None):
     if args.only in (None, "prefill"):
         log("[bench] config 4: prefix-cached prefill (Qwen3-8B heads)")
         c4 = W.config4(dev)
-        out["cfg4"] = bench_prefill(c4, max(10, steps // 2), warmup)
+        out["cfg4"] = bench_prefill(c4, max(10, steps // 2), warmup, args.warm_seconds)
         log(f"[bench] cfg4 {out['cfg4']['ms']*1e3:.1f} us = {out['cfg4']['tflops']:.0f} TFLOP/s")
         del c4
         log("[bench] config 2: varlen prefill")
         c2 = W.config2(dev)
-        out["cfg2"] = bench_prefill(c2, max(10, steps // 2), warmup)
+        out["cfg2"] = bench_prefill(c2, max(10, steps // 2), warmup, args.warm_seconds)
         log(f"[bench] cfg2 {out['cfg2']['ms']*1e3:.1f} us = {out['cfg2']['tflops']:.0f} TFLOP/s")
         del c2
         torch.cuda.empty_cache()
     if args.only in (None, "fp8"):
         log("[bench] config 5: fp8 KV decode, B=64, ctx U[16k,32k]")
         c5 = W.config5(dev)
-        out["cfg5"] = bench_decode(c5, max(10, steps // 2), warmup)
+        out["cfg5"] = bench_decode(c5, max(10, steps // 2), warmup, warm_s=args.warm_seconds)
         log(f"[bench] cfg5 attention {out['cfg5']['attn_ms']*1e3:.1f} us = {out['cfg5']['attn_gbs']:.0f} GB/s")
         del c5
         torch.cuda.empty_cache()
