@@ -7,11 +7,11 @@ context U[100, 2048], 2048-page pool).  A step is one such pass with inputs
 resident in HBM; consecutive steps alternate between independent cache pools so
 the 256 MB Infinity Cache cannot serve them.  Alongside: prefill TFLOP/s
 (config 4 prefix-cached, Qwen3-8B heads 32/8; config 2 varlen), fp8-KV decode
-GB/s (config 5), the roofline of the dominant kernel (HIP events on the launch
+GB/s (config 5), the fused qk-RMSNorm + rotary producer step (GB/s), the roofline of the dominant kernel (HIP events on the launch
 stream) and the PyTorch CPU baseline (gather + SDPA) on the host cores.
 
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--warm-seconds 1] [--no-cpu]
-                       [--only decode|prefill|fp8]
+                       [--only decode|prefill|fp8|producer]
 """
 from __future__ import annotations
 
@@ -143,6 +143,27 @@ def bench_prefill(case, steps, warmup, warm_s=1.0):
     return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
 
 
+def bench_producer(case, steps, warmup, warm_s=1.0):
+    """The fused qk-RMSNorm + rotary step (nva_qk_norm_rope) over config 4's tokens."""
+    import torch
+    from nanovllm_amd.layers.qk_norm_rope import qk_norm_rope
+
+    def run(i=0):
+        return qk_norm_rope(case.positions, case.q, case.k, case.cos_sin_cache, case.num_heads,
+                            case.num_kv_heads, case.head_dim, case.q_norm_weight, case.k_norm_weight, case.eps)
+
+    _warm(run, warmup, warm_s)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record()
+        run()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    nbytes = case.bytes()
+    return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9)
+
+
 def cpu_baseline_decode(case_gpu, budget_s=20.0):
     """Reference-semantics PyTorch CPU decode step on a bounded sample of config 3."""
     import torch
@@ -183,7 +204,7 @@ def main(argv=None):
     ap.add_argument("--warm-seconds", type=float, default=1.0,
                     help="after the warmup steps, keep running each workload untimed for this long")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["decode", "prefill", "fp8"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "fp8", "producer"], default=None)
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args(argv)
@@ -232,6 +253,13 @@ def main(argv=None):
         log(f"[bench] cfg2 {out['cfg2']['ms']*1e3:.1f} us = {out['cfg2']['tflops']:.0f} TFLOP/s")
         del c2
         torch.cuda.empty_cache()
+    if args.only in (None, "producer"):
+        log("[bench] producer: fused qk-RMSNorm + rotary over config 4's 8813 tokens (heads 32/8)")
+        cp = W.producer_config4(dev)
+        out["producer"] = bench_producer(cp, max(10, steps // 2), warmup, args.warm_seconds)
+        log(f"[bench] producer {out['producer']['ms']*1e3:.1f} us = {out['producer']['gbs']:.0f} GB/s")
+        del cp
+        torch.cuda.empty_cache()
     if args.only in (None, "fp8"):
         log("[bench] config 5: fp8 KV decode, B=64, ctx U[16k,32k]")
         c5 = W.config5(dev)
@@ -269,6 +297,11 @@ def main(argv=None):
         line["fp8_decode"] = {"cfg5": {"gbs": round(d5["attn_gbs"], 1), "frac": round(d5["attn_gbs"] / HBM_PEAK_GBS, 4),
                                        "attn_us": round(d5["attn_ms"] * 1e3, 2), "bytes": d5["attn_bytes"],
                                        "traffic": profiled_traffic("config5")}}
+    if "producer" in out:
+        dp = out["producer"]
+        line["qk_norm_rope"] = {"workload": "config 4 tokens, heads 32/8, head_dim 128",
+                                "gbs": round(dp["gbs"], 1), "frac": round(dp["gbs"] / HBM_PEAK_GBS, 4),
+                                "us": round(dp["ms"] * 1e3, 2), "bytes": dp["bytes"]}
     if "value" not in line:
         k = next(iter(out))
         line["value"] = None

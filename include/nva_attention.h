@@ -126,6 +126,30 @@ int nva_decode(const void* q, int64_t q_row_stride,
                void* out, int64_t out_row_stride,
                void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * Fused per-head RMSNorm + rotary embedding of q and k: the producer step feeding the
+ * path.  Replaces, in Qwen3Attention.forward (qwen3.py:91-105),
+ *   q = q_norm(q.view(T, nh, d)); k = k_norm(k.view(T, nkv, d))   layernorm.py:17-27
+ *   q, k = rotary_emb(positions, q, k)                             rotary_embedding.py:37-55
+ * q/k: (num_tokens, heads, head_dim) bf16 rows with head stride head_dim and free row
+ * strides (views into the fused qkv projection, qwen3.py:89); outputs have the same
+ * layout and may alias the inputs (in place).  q_norm_weight/k_norm_weight: bf16
+ * (head_dim,), both NULL for the rotary embedding alone (Qwen2, qwen2.py:91-92).
+ * cos_sin_cache: fp32 (max_position, head_dim), row p = [cos(p*f) | sin(p*f)] as
+ * RotaryEmbedding builds it (rotary_embedding.py:29-35); positions: int64 (num_tokens,),
+ * clamped to [0, max_position).  head_dim 64 or 128.  Results follow the reference's
+ * eager rounding steps; the sum of squares runs in a different order, so an output can
+ * differ from the reference's by one bf16 ulp.
+ */
+int nva_qk_norm_rope(const void* q, int64_t q_row_stride,
+                     const void* k, int64_t k_row_stride,
+                     void* q_out, int64_t q_out_row_stride,
+                     void* k_out, int64_t k_out_row_stride,
+                     const void* q_norm_weight, const void* k_norm_weight, float eps,
+                     const float* cos_sin_cache, int64_t max_position,
+                     const int64_t* positions, int64_t num_tokens,
+                     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -271,4 +271,59 @@ int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const v
   return hip_status(nva::launch_decode(p, kv_dtype, static_cast<hipStream_t>(stream)), "decode launch");
 }
 
+int nva_qk_norm_rope(const void* q, int64_t q_row_stride, const void* k, int64_t k_row_stride, void* q_out,
+                     int64_t q_out_row_stride, void* k_out, int64_t k_out_row_stride, const void* q_norm_weight,
+                     const void* k_norm_weight, float eps, const float* cos_sin_cache, int64_t max_position,
+                     const int64_t* positions, int64_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                     int32_t head_dim, void* stream) {
+  if (num_tokens < 0) return fail(NVA_ERR_INVALID_ARGUMENT, "num_tokens must be >= 0 (got %lld)", (long long)num_tokens);
+  if (num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "num_heads, num_kv_heads and head_dim must be positive");
+  if (head_dim != 64 && head_dim != 128)
+    return fail(NVA_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", head_dim);
+  if ((q_norm_weight == nullptr) != (k_norm_weight == nullptr))
+    return fail(NVA_ERR_INVALID_ARGUMENT, "pass both norm weights (qk-norm) or neither (rotary embedding only)");
+  if (q_norm_weight && !(eps >= 0.f)) return fail(NVA_ERR_INVALID_ARGUMENT, "eps must be >= 0");
+  if (max_position <= 0) return fail(NVA_ERR_INVALID_ARGUMENT, "max_position must be positive");
+  if (num_tokens == 0) return ok();
+  if (!q || !k || !q_out || !k_out || !cos_sin_cache || !positions)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  const int64_t hd = static_cast<int64_t>(num_heads) * head_dim;
+  const int64_t kd = static_cast<int64_t>(num_kv_heads) * head_dim;
+  if (q_row_stride < hd || q_out_row_stride < hd)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "q/q_out row strides must be >= num_heads*head_dim");
+  if (k_row_stride < kd || k_out_row_stride < kd)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "k/k_out row strides must be >= num_kv_heads*head_dim");
+  const uintptr_t a = head_dim == 128 ? 8 : 4;  // bytes each lane moves per half row
+  if (!aligned(q, a) || !aligned(k, a) || !aligned(q_out, a) || !aligned(k_out, a) ||
+      (q_norm_weight && (!aligned(q_norm_weight, a) || !aligned(k_norm_weight, a))) ||
+      (q_row_stride * 2) % a || (k_row_stride * 2) % a || (q_out_row_stride * 2) % a || (k_out_row_stride * 2) % a)
+    return fail(NVA_ERR_UNSUPPORTED, "q/k rows and weights must be %d-byte aligned", (int)a);
+  if (!aligned(cos_sin_cache, 4) || !aligned(positions, 8))
+    return fail(NVA_ERR_INVALID_ARGUMENT, "cos_sin_cache must be 4-byte and positions 8-byte aligned");
+  if (num_tokens * (num_heads + num_kv_heads) > (int64_t{1} << 36))
+    return fail(NVA_ERR_UNSUPPORTED, "num_tokens*(num_heads+num_kv_heads) above 2^36");
+
+  nva::QKNormRopeParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.q_out = static_cast<uint16_t*>(q_out);
+  p.k_out = static_cast<uint16_t*>(k_out);
+  p.q_weight = static_cast<const uint16_t*>(q_norm_weight);
+  p.k_weight = static_cast<const uint16_t*>(k_norm_weight);
+  p.cos_sin = cos_sin_cache;
+  p.positions = positions;
+  p.q_row_stride = q_row_stride;
+  p.k_row_stride = k_row_stride;
+  p.q_out_row_stride = q_out_row_stride;
+  p.k_out_row_stride = k_out_row_stride;
+  p.num_tokens = num_tokens;
+  p.max_position = max_position;
+  p.num_heads = num_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.head_dim = head_dim;
+  p.eps = eps;
+  return hip_status(nva::launch_qk_norm_rope(p, static_cast<hipStream_t>(stream)), "qk_norm_rope launch");
+}
+
 }  // extern "C"

@@ -77,7 +77,24 @@ struct PrefillParams {
   float scale_log2;
 };
 
+struct QKNormRopeParams {
+  const uint16_t* q;          // (T, nh, d) bf16, head stride d
+  const uint16_t* k;          // (T, nkv, d) bf16, head stride d
+  uint16_t* q_out;            // may alias q
+  uint16_t* k_out;            // may alias k
+  const uint16_t* q_weight;   // (d,) bf16 q_norm weight, or null: rotary embedding only
+  const uint16_t* k_weight;   // (d,) bf16 k_norm weight (null iff q_weight is)
+  const float* cos_sin;       // (max_position, d) fp32: [cos(d/2) | sin(d/2)] per position
+  const int64_t* positions;   // (T,)
+  int64_t q_row_stride, k_row_stride, q_out_row_stride, k_out_row_stride;
+  int64_t num_tokens;
+  int64_t max_position;
+  int32_t num_heads, num_kv_heads, head_dim;
+  float eps;
+};
+
 hipError_t launch_store_kvcache(const StoreParams& p, int vec_bytes, hipStream_t stream);
+hipError_t launch_qk_norm_rope(const QKNormRopeParams& p, hipStream_t stream);
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, hipStream_t stream);
 hipError_t launch_prefill(const PrefillParams& p, int max_seqlen_q, hipStream_t stream);
 int prefill_positions_per_tile(int group);  // query positions one prefill workgroup covers

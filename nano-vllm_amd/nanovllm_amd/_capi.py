@@ -55,6 +55,13 @@ SIGNATURES = {
         _c_void_p, _i64,                   # out, out_row_stride
         _c_void_p, _i64, _c_void_p,        # workspace, workspace_bytes, stream
     ]),
+    "nva_qk_norm_rope": (_i32, [
+        _c_void_p, _i64, _c_void_p, _i64,  # q, q_row_stride, k, k_row_stride
+        _c_void_p, _i64, _c_void_p, _i64,  # q_out, q_out_row_stride, k_out, k_out_row_stride
+        _c_void_p, _c_void_p, _f32,        # q_norm_weight, k_norm_weight, eps
+        _c_void_p, _i64, _c_void_p, _i64,  # cos_sin_cache, max_position, positions, num_tokens
+        _i32, _i32, _i32, _c_void_p,       # num_heads, num_kv_heads, head_dim, stream
+    ]),
 }
 
 

@@ -297,3 +297,64 @@ def config5(bulk_device="cpu", seed=SEEDS[5]) -> DecodeCase:
 
 
 CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
+
+
+@dataclass
+class ProducerCase:
+    """Inputs of the fused qk-RMSNorm + rotary step (qwen3.py:91-105): q and k are
+    views into one fused qkv buffer, as the qkv projection leaves them."""
+    name: str
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    qkv: torch.Tensor              # (T, (nh + 2 nkv) d) bf16
+    q: torch.Tensor                # (T, nh, d) view
+    k: torch.Tensor                # (T, nkv, d) view
+    positions: torch.Tensor        # (T,) int64
+    cos_sin_cache: torch.Tensor    # (max_position, d) fp32
+    q_norm_weight: torch.Tensor | None
+    k_norm_weight: torch.Tensor | None
+    eps: float = 1e-6
+
+    @property
+    def num_tokens(self) -> int:
+        return self.q.shape[0]
+
+    def bytes(self) -> int:
+        """Algorithmic HBM bytes of one fused call: q and k rows read and written once
+        (bf16), one cos/sin row (fp32) and one int64 position per token, the weights."""
+        rows = self.num_tokens * (self.num_heads + self.num_kv_heads)
+        w = 0 if self.q_norm_weight is None else 2 * self.head_dim * 2
+        return rows * self.head_dim * 2 * 2 + self.num_tokens * (self.head_dim * 4 + 8) + w
+
+
+def make_producer_case(num_tokens, num_heads, num_kv_heads, *, head_dim=128, max_position=40960,
+                       rope_theta=1_000_000.0, norm=True, positions=None, seed=0, device="cpu",
+                       name="producer") -> ProducerCase:
+    """Qwen3 defaults (rope_theta 1e6, max_position 40960, eps 1e-6, qwen3.py:156-160);
+    norm=False gives the Qwen2 rotary-only step.  Positions default to uniform random."""
+    from .layers.qk_norm_rope import rope_cos_sin_cache
+    gen = torch.Generator(device=device).manual_seed(seed * 7919 + 29)
+    T, nh, nkv, d = num_tokens, num_heads, num_kv_heads, head_dim
+    qkv = _randn_bf16((T, (nh + 2 * nkv) * d), gen, device)
+    q = qkv[:, : nh * d].view(T, nh, d)
+    k = qkv[:, nh * d:(nh + nkv) * d].view(T, nkv, d)
+    if positions is None:
+        positions = torch.randint(0, max_position, (T,), generator=gen, device=device, dtype=torch.int64)
+    else:
+        positions = torch.as_tensor(positions, dtype=torch.int64, device=device)
+    cache = rope_cos_sin_cache(d, max_position, rope_theta, device=device)
+    wq = wk = None
+    if norm:
+        wq = (1.0 + 0.2 * torch.randn(d, generator=gen, device=device)).to(BF16)
+        wk = (1.0 + 0.2 * torch.randn(d, generator=gen, device=device)).to(BF16)
+    return ProducerCase(name, nh, nkv, d, qkv, q, k, positions, cache, wq, wk)
+
+
+def producer_config4(device="cpu", seed=SEEDS[4]) -> ProducerCase:
+    """The producer step for config 4's suffix tokens: Qwen3-8B heads 32/8, positions
+    1024 + i within each sequence (the cached prefix comes first)."""
+    gen = torch.Generator().manual_seed(seed)
+    lens = torch.randint(256, 769, (16,), generator=gen).tolist()
+    pos = [1024 + i for L in lens for i in range(L)]
+    return make_producer_case(len(pos), 32, 8, positions=pos, seed=seed, device=device, name="producer-cfg4")

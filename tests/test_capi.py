@@ -34,7 +34,7 @@ def declared_functions():
 def test_header_lists_entry_points():
     names = declared_functions()
     assert {"nva_store_kvcache", "nva_prefill", "nva_decode", "nva_decode_workspace_bytes",
-            "nva_last_error", "nva_version"} <= set(names)
+            "nva_last_error", "nva_version", "nva_qk_norm_rope"} <= set(names)
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -168,3 +168,36 @@ def test_error_raises_runtime_error(lib):
     assert decode(lib, head_dim=64) != 0
     with pytest.raises(RuntimeError, match="head_dim"):
         _capi.check(_capi.NVA_ERR_UNSUPPORTED)
+
+
+def qk_norm_rope(lib, **kw):
+    args = dict(q=A, q_row_stride=6144, k=A + 0x1000, k_row_stride=6144, q_out=B, q_out_row_stride=4096,
+                k_out=C, k_out_row_stride=1024, q_w=A + 0x20000, k_w=A + 0x20100, eps=1e-6,
+                cos_sin=A + 0x40000, max_position=4096, positions=A + 0x80000, num_tokens=5, num_heads=32,
+                num_kv_heads=8, head_dim=128, stream=None)
+    args.update(kw)
+    return lib.nva_qk_norm_rope(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(num_tokens=-1), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(num_heads=0), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(head_dim=96), _capi.NVA_ERR_UNSUPPORTED),
+    (dict(k_w=None), _capi.NVA_ERR_INVALID_ARGUMENT),               # one weight without the other
+    (dict(eps=-1.0), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(max_position=0), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(positions=None), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(q_row_stride=4000), _capi.NVA_ERR_INVALID_ARGUMENT),       # < num_heads * head_dim
+    (dict(k_out_row_stride=1000), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(q=A + 4), _capi.NVA_ERR_UNSUPPORTED),                      # head_dim 128 needs 8-byte rows
+    (dict(positions=A + 0x80004), _capi.NVA_ERR_INVALID_ARGUMENT),
+])
+def test_qk_norm_rope_rejects(lib, kw, code):
+    assert qk_norm_rope(lib, **kw) == code
+    assert lib.nva_last_error().decode()
+
+
+def test_qk_norm_rope_zero_tokens_is_noop(lib):
+    assert qk_norm_rope(lib, num_tokens=0, q=None) == _capi.NVA_OK
+    # rotary embedding only (no weights) and head_dim 64 validate too
+    assert qk_norm_rope(lib, num_tokens=0, q_w=None, k_w=None, head_dim=64) == _capi.NVA_OK
