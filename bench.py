@@ -11,7 +11,7 @@ GB/s (config 5), the fused qk-RMSNorm + rotary producer step (GB/s), the rooflin
 stream) and the PyTorch CPU baseline (gather + SDPA) on the host cores.
 
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--warm-seconds 1] [--no-cpu]
-                       [--only decode|prefill|fp8|producer]
+                       [--only decode|prefill|fp8|producer|graphs]
 """
 from __future__ import annotations
 
@@ -164,6 +164,47 @@ def bench_producer(case, steps, warmup, warm_s=1.0):
     return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9)
 
 
+def bench_graph_decode(dev, steps, warmup, warm_s=1.0, layers=28, ctx=1024, batch_sizes=(1, 16, 64, 256)):
+    """Captured decode steps (nanovllm_amd.engine.decode_graphs, the capture_cudagraph /
+    run_model mirror) of `layers` Qwen3-0.6B attention layers (heads 16/8, head_dim 128)
+    at a fixed context: one run() = buffer refresh + one graph replay of store + decode
+    for every layer.  Caches are zero-filled (the timing does not depend on values)."""
+    import torch
+    import nanovllm_amd as nva
+    from nanovllm_amd.engine.decode_graphs import DecodeGraphs
+    nh, nkv, d, bsz = 16, 8, 128, 256
+    max_bs = max(batch_sizes)
+    pages_per_seq = ctx // bsz + 1
+    num_blocks = max_bs * pages_per_seq
+    attn = []
+    for _ in range(layers):
+        a = nva.Attention(nh, d, d ** -0.5, nkv)
+        a.k_cache = torch.zeros(num_blocks, bsz, nkv, d, dtype=torch.bfloat16, device=dev)
+        a.v_cache = torch.zeros_like(a.k_cache)
+        attn.append(a)
+    graphs = DecodeGraphs(attn, max_bs=max_bs, max_num_blocks=pages_per_seq).capture()
+    res = {}
+    for bs in batch_sizes:
+        q = torch.randn(bs, nh * d, device=dev).bfloat16()
+        k = torch.randn(bs, nkv * d, device=dev).bfloat16()
+        v = torch.randn(bs, nkv * d, device=dev).bfloat16()
+        bt = torch.arange(bs * pages_per_seq, dtype=torch.int32, device=dev).view(bs, pages_per_seq)
+        ctx_t = torch.full((bs,), ctx, dtype=torch.int32, device=dev)
+        slots = (bt[:, (ctx - 1) // bsz] * bsz + (ctx - 1) % bsz).contiguous()
+        _warm(lambda i: graphs.run(q, k, v, slots, ctx_t, bt), warmup, warm_s / len(batch_sizes))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            graphs.run(q, k, v, slots, ctx_t, bt)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        kv = bs * ctx * nkv * d * 2 * 2 * layers
+        res[bs] = dict(step_us=round(us, 1), layer_us=round(us / layers, 2), kv_gbs=round(kv / (us * 1e-6) / 1e9, 1))
+    del graphs, attn
+    return res
+
+
 def cpu_baseline_decode(case_gpu, budget_s=20.0):
     """Reference-semantics PyTorch CPU decode step on a bounded sample of config 3."""
     import torch
@@ -204,7 +245,7 @@ def main(argv=None):
     ap.add_argument("--warm-seconds", type=float, default=1.0,
                     help="after the warmup steps, keep running each workload untimed for this long")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["decode", "prefill", "fp8", "producer"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "fp8", "producer", "graphs"], default=None)
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args(argv)
@@ -260,6 +301,13 @@ def main(argv=None):
         log(f"[bench] producer {out['producer']['ms']*1e3:.1f} us = {out['producer']['gbs']:.0f} GB/s")
         del cp
         torch.cuda.empty_cache()
+    if args.only in (None, "graphs"):
+        log("[bench] graph decode: captured store + decode steps of 28 layers (heads 16/8), context 1024")
+        out["graphs"] = bench_graph_decode(dev, max(10, steps // 5), warmup, args.warm_seconds)
+        for bs, r in out["graphs"].items():
+            log(f"[bench] graph decode bs={bs}: {r['step_us']} us/step ({r['layer_us']} us/layer, "
+                f"{r['kv_gbs']} GB/s of KV)")
+        torch.cuda.empty_cache()
     if args.only in (None, "fp8"):
         log("[bench] config 5: fp8 KV decode, B=64, ctx U[16k,32k]")
         c5 = W.config5(dev)
@@ -297,6 +345,10 @@ def main(argv=None):
         line["fp8_decode"] = {"cfg5": {"gbs": round(d5["attn_gbs"], 1), "frac": round(d5["attn_gbs"] / HBM_PEAK_GBS, 4),
                                        "attn_us": round(d5["attn_ms"] * 1e3, 2), "bytes": d5["attn_bytes"],
                                        "traffic": profiled_traffic("config5")}}
+    if "graphs" in out:
+        line["graph_decode"] = {"workload": "28 layers x (store + paged decode), heads 16/8, head_dim 128, "
+                                            "context 1024, HIP graph per batch size",
+                                "per_batch": {str(k): v for k, v in out["graphs"].items()}}
     if "producer" in out:
         dp = out["producer"]
         line["qk_norm_rope"] = {"workload": "config 4 tokens, heads 32/8, head_dim 128",

@@ -489,29 +489,42 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
     count = (ctx + p.keys_per_split - 1) / p.keys_per_split;
     zero = count == 0;
   }
+  // A partial slot holds data unless it is a balanced range with no steps (P > T).
+  const int64_t T = p.balanced_ranges > 0 ? p.ws_prefix[p.batch] : 0;
+  auto has_data = [&](int64_t s) {
+    if (p.balanced_ranges <= 0) return true;
+    const int64_t rr = first - b + s;
+    return range_start(rr, T, p.balanced_ranges) != range_start(rr + 1, T, p.balanced_ranges);
+  };
+  // pass 1: the maximum over the partials, lanes in parallel
   float M = kNegInf;
-  for (int64_t s = 0; s < count; ++s) {
-    if (p.balanced_ranges > 0) {  // ranges that are empty (P > T) wrote nothing
-      const int64_t rr = first - b + s;
-      const int64_t T = p.ws_prefix[p.batch];
-      if (range_start(rr, T, p.balanced_ranges) == range_start(rr + 1, T, p.balanced_ranges)) continue;
-    }
-    M = fmaxf(M, p.ws_ml[((first + s) * p.num_heads + h) * 2]);
-  }
+  if (!zero)
+    for (int64_t s = lane; s < count; s += 64)
+      if (has_data(s)) M = fmaxf(M, p.ws_ml[((first + s) * p.num_heads + h) * 2]);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, shfl_xor(M, m));
+  // pass 2: weighted sums, eight partials' loads in flight at a time
   float L = 0.f, o0 = 0.f, o1 = 0.f;
   if (!zero && M != kNegInf) {
-    for (int64_t s = 0; s < count; ++s) {
-      if (p.balanced_ranges > 0) {
-        const int64_t rr = first - b + s;
-        const int64_t T = p.ws_prefix[p.batch];
-        if (range_start(rr, T, p.balanced_ranges) == range_start(rr + 1, T, p.balanced_ranges)) continue;
+    for (int64_t s0 = 0; s0 < count; s0 += 8) {
+      float w[8], l[8];
+      f32x2 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t s = s0 + u;
+        const bool ok = s < count && has_data(s);
+        const int64_t idx = (first + (ok ? s : 0)) * p.num_heads + h;
+        const f32x2 ml = ok ? *reinterpret_cast<const f32x2*>(p.ws_ml + idx * 2) : f32x2{kNegInf, 0.f};
+        w[u] = ok ? fast_exp2(ml[0] - M) : 0.f;
+        l[u] = ml[1];
+        v[u] = ok ? *reinterpret_cast<const f32x2*>(p.ws_o + idx * kHeadDim + 2 * lane) : f32x2{0.f, 0.f};
       }
-      const int64_t idx = (first + s) * p.num_heads + h;
-      const float w = fast_exp2(p.ws_ml[idx * 2] - M);
-      L += w * p.ws_ml[idx * 2 + 1];
-      const f32x2 v = *reinterpret_cast<const f32x2*>(p.ws_o + idx * kHeadDim + 2 * lane);
-      o0 += w * v[0];
-      o1 += w * v[1];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        L += w[u] * l[u];
+        o0 += w[u] * v[u][0];
+        o1 += w[u] * v[u][1];
+      }
     }
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;

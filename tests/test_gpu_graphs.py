@@ -1,0 +1,107 @@
+"""The decode graph harness (nanovllm_amd.engine.decode_graphs) on the GPU: captured
+steps of two Attention layers replayed at several batch sizes match eager
+execution, padded rows leave the cache alone (slot pad -1, reference quirk Q1),
+and sizes beyond the largest graph run eagerly."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import assert_attn_close, f32
+
+pytestmark = pytest.mark.gpu
+
+NH, NKV, D, BS_PAGE = 16, 8, 128, 256
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need an MI355X"
+    from nanovllm_amd import _capi
+    _capi.load()
+    return torch.device("cuda:0")
+
+
+def _layers(dev, n_layers, num_blocks, seed):
+    import nanovllm_amd as nva
+    g = torch.Generator(device=dev).manual_seed(seed)
+    layers = []
+    for _ in range(n_layers):
+        a = nva.Attention(NH, D, D ** -0.5, NKV)
+        a.k_cache = torch.randn(num_blocks, BS_PAGE, NKV, D, generator=g, device=dev).bfloat16()
+        a.v_cache = torch.randn(num_blocks, BS_PAGE, NKV, D, generator=g, device=dev).bfloat16()
+        layers.append(a)
+    return layers
+
+
+def _batch(dev, bs, max_blocks, num_blocks, seed):
+    g = torch.Generator().manual_seed(seed)
+    ctx = torch.randint(1, max_blocks * BS_PAGE, (bs,), generator=g)
+    perm = torch.randperm(num_blocks, generator=g)
+    bt = torch.full((bs, max_blocks), -1, dtype=torch.int32)
+    slots = []
+    at = 0
+    for b in range(bs):
+        n = math.ceil(int(ctx[b]) / BS_PAGE)
+        bt[b, :n] = perm[at:at + n].to(torch.int32)
+        at += n
+        last = int(ctx[b]) - 1
+        slots.append(int(bt[b, last // BS_PAGE]) * BS_PAGE + last % BS_PAGE)
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    q = torch.randn(bs, NH * D, generator=gd, device=dev).bfloat16()
+    k = torch.randn(bs, NKV * D, generator=gd, device=dev).bfloat16()
+    v = torch.randn(bs, NKV * D, generator=gd, device=dev).bfloat16()
+    return (q, k, v, torch.tensor(slots, dtype=torch.int32, device=dev), ctx.to(torch.int32).to(dev),
+            bt.to(dev))
+
+
+def _eager(layers, q, k, v, slots, ctx, bt):
+    import nanovllm_amd as nva
+    nva.set_context(False, slot_mapping=slots, context_lens=ctx, block_tables=bt)
+    try:
+        return torch.stack([a(q, k, v) for a in layers])
+    finally:
+        nva.reset_context()
+
+
+def test_replay_matches_eager_and_skips_padding(dev):
+    from nanovllm_amd.engine.decode_graphs import DecodeGraphs
+    max_blocks, num_blocks = 4, 160
+    layers = _layers(dev, 2, num_blocks, seed=3)
+    # page 0's first slot holds a sentinel a zero-padded slot mapping would overwrite
+    for a in layers:
+        a.k_cache[0, 0].fill_(7.0)
+        a.v_cache[0, 0].fill_(-7.0)
+    twins = _layers(dev, 2, num_blocks, seed=3)
+    for a in twins:
+        a.k_cache[0, 0].fill_(7.0)
+        a.v_cache[0, 0].fill_(-7.0)
+    graphs = DecodeGraphs(layers, max_bs=48, max_num_blocks=max_blocks).capture()
+    assert sorted(graphs.graphs) == [1, 2, 4, 8, 16, 32, 48]
+    for i, bs in enumerate([1, 3, 16, 17, 40, 48]):
+        batch = _batch(dev, bs, max_blocks - 1, num_blocks, seed=100 + i)
+        got = graphs.run(*batch)
+        ref = _eager(twins, *batch)
+        torch.cuda.synchronize()
+        assert got.shape == (2, bs, NH * D)
+        # the padded launch plans its split-K for the graph size, so sums may round differently
+        assert_attn_close(f32(got), f32(ref), what=f"graph bs={bs}")
+        for a, t in zip(layers, twins):  # same cache contents: the live rows' store
+            assert torch.equal(a.k_cache, t.k_cache) and torch.equal(a.v_cache, t.v_cache)
+        for a in layers:
+            assert bool((a.k_cache[0, 0] == 7.0).all()) and bool((a.v_cache[0, 0] == -7.0).all())
+
+
+def test_batches_beyond_the_graphs_run_eagerly(dev):
+    from nanovllm_amd.engine.decode_graphs import DecodeGraphs
+    layers = _layers(dev, 1, 40, seed=5)
+    twins = _layers(dev, 1, 40, seed=5)
+    graphs = DecodeGraphs(layers, max_bs=8, max_num_blocks=2).capture()
+    batch = _batch(dev, 12, 2, 40, seed=9)
+    got = graphs.run(*batch)
+    ref = _eager(twins, *batch)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
