@@ -113,7 +113,8 @@ int nva_prefill(const void* q, int64_t q_row_stride, const void* k, int64_t k_ro
                 int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads, int32_t num_kv_heads,
                 int32_t head_dim, float softmax_scale, void* out, int64_t out_row_stride, void* stream) {
   (void)max_seqlen_k;
-  if (head_dim != 128) return fail(NVA_ERR_UNSUPPORTED, "head_dim %d not supported (128 only)", head_dim);
+  if (head_dim != 128 && head_dim != 64)
+    return fail(NVA_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", head_dim);
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
     return fail(NVA_ERR_INVALID_ARGUMENT, "num_heads (%d) must be a positive multiple of num_kv_heads (%d)", num_heads, num_kv_heads);
   if (num_heads > 65535) return fail(NVA_ERR_UNSUPPORTED, "num_heads above 65535");
@@ -170,6 +171,7 @@ int nva_prefill(const void* q, int64_t q_row_stride, const void* k, int64_t k_ro
   p.num_heads = num_heads;
   p.num_kv_heads = num_kv_heads;
   p.group = num_heads / num_kv_heads;
+  p.head_dim = head_dim;
   p.scale_log2 = softmax_scale * kLog2e;
   return hip_status(nva::launch_prefill(p, max_seqlen_q, static_cast<hipStream_t>(stream)), "prefill launch");
 }
@@ -195,7 +197,8 @@ int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const v
                int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
                int32_t num_splits, void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
                void* stream) {
-  if (head_dim != 128) return fail(NVA_ERR_UNSUPPORTED, "head_dim %d not supported (128 only)", head_dim);
+  if (head_dim != 128 && head_dim != 64)
+    return fail(NVA_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", head_dim);
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
     return fail(NVA_ERR_INVALID_ARGUMENT, "num_heads (%d) must be a positive multiple of num_kv_heads (%d)", num_heads, num_kv_heads);
   if (num_heads / num_kv_heads > 16)
@@ -203,6 +206,10 @@ int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const v
   if (num_kv_heads > 65535) return fail(NVA_ERR_UNSUPPORTED, "num_kv_heads above 65535");
   if (kv_dtype != NVA_DTYPE_BF16 && kv_dtype != NVA_DTYPE_FP8_E4M3)
     return fail(NVA_ERR_INVALID_ARGUMENT, "unknown kv dtype %d", kv_dtype);
+  // fp8 decode at head_dim 64 faulted on the GPU (an address outside every
+  // aperture) for a cause not yet found; it stays refused until then.
+  if (kv_dtype == NVA_DTYPE_FP8_E4M3 && head_dim != 128)
+    return fail(NVA_ERR_UNSUPPORTED, "fp8 kv cache decode supports head_dim 128 only");
   if (batch < 0) return fail(NVA_ERR_INVALID_ARGUMENT, "batch must be >= 0");
   if (batch > 65535) return fail(NVA_ERR_UNSUPPORTED, "batch above 65535");
   if (num_splits < 0) return fail(NVA_ERR_INVALID_ARGUMENT, "num_splits must be >= 0");
@@ -267,6 +274,7 @@ int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const v
   p.keys_per_split = plan.pages_per_split * block_size;
   p.num_splits = plan.num_splits;
   p.balanced_ranges = plan.balanced_ranges;
+  p.head_dim = head_dim;
   p.scale_log2 = softmax_scale * kLog2e;
   return hip_status(nva::launch_decode(p, kv_dtype, static_cast<hipStream_t>(stream)), "decode launch");
 }

@@ -25,15 +25,15 @@ struct StoreParams {
 };
 
 struct DecodeParams {
-  const uint16_t* q;          // (B, nh, 128) bf16, head stride 128
-  const void* k_cache;        // (num_blocks, block_size, nkv, 128)
+  const uint16_t* q;          // (B, nh, d) bf16, head stride d
+  const void* k_cache;        // (num_blocks, block_size, nkv, d)
   const void* v_cache;
   const float* k_scale;       // [nkv] (fp8) or null
   const float* v_scale;
   const int32_t* seqlens;     // [B]
   const int32_t* block_table; // [B, bt_row_stride]
-  uint16_t* out;              // (B, nh, 128) bf16
-  float* ws_o;                // [slots, nh, 128] partial numerators
+  uint16_t* out;              // (B, nh, d) bf16
+  float* ws_o;                // [slots, nh, d] partial numerators
   float* ws_ml;               // [slots, nh, 2] partial (max, sum)
   int32_t* ws_prefix;         // [B + 1] step prefix (balanced mode)
   int64_t q_row_stride;
@@ -49,17 +49,18 @@ struct DecodeParams {
   int32_t keys_per_split;     // fixed mode: multiple of block_size
   int32_t num_splits;         // fixed mode: splits per sequence
   int32_t balanced_ranges;    // balanced mode: number of step ranges P (0 = fixed mode)
+  int32_t head_dim;           // 64 or 128
   float scale_log2;           // softmax_scale * log2(e)
 };
 
 struct PrefillParams {
-  const uint16_t* q;          // (Tq, nh, 128) bf16
-  const uint16_t* k;          // packed (Tk, nkv, 128) or cache (slots, nkv, 128)
+  const uint16_t* q;          // (Tq, nh, d) bf16
+  const uint16_t* k;          // packed (Tk, nkv, d) or cache (slots, nkv, d)
   const uint16_t* v;
   const int32_t* block_table; // null => packed
   const int32_t* cu_q;        // [S+1]
   const int32_t* cu_k;        // [S+1]
-  uint16_t* out;              // (Tq, nh, 128)
+  uint16_t* out;              // (Tq, nh, d)
   int64_t q_row_stride;
   int64_t k_row_stride;
   int64_t v_row_stride;
@@ -74,6 +75,7 @@ struct PrefillParams {
   int32_t group;
   int32_t num_q_tiles;        // ceil(max_seqlen_q / positions_per_tile)
   int32_t positions_per_tile; // query positions per workgroup (x group = rows)
+  int32_t head_dim;           // 64 or 128
   float scale_log2;
 };
 

@@ -49,16 +49,23 @@ constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kTau = 8.0f;                  // lazy-rescale threshold (log2 units)
 constexpr float kInitMax = -1e30f;            // finite: exp2(fma(s, c, -m)) never sees -inf - -inf
 
-// K: 16-byte piece swizzle; the 16 consecutive rows one quarter-wave of an
-// operand read touches land in 16 distinct bank groups.
-__device__ __forceinline__ int k_swz(int row) { return row & 15; }
-// V: 32-byte chunk swizzle; each half-wave of a transposing read (4 rows x 2
-// chunks) lands in 8 distinct 32-byte bank groups.
-__device__ __forceinline__ int v_swz(int row) { return 2 * (row & 3); }
+constexpr int kStages = 4;                    // LDS ring depth
 
-constexpr int kTileBytes = kBK * kHeadDim * 2;  // one K (or V) tile: 16 KiB
-constexpr int kStageBytes = 2 * kTileBytes;      // K + V
-constexpr int kStages = 4;                        // LDS ring depth (128 KiB)
+// Tile geometry for head dimension D (64 or 128): a key row is RB = 2D bytes.
+template <int D>
+struct Geom {
+  static constexpr int RB = 2 * D;
+  static constexpr int kTileBytes = kBK * RB;        // one K (or V) tile: 16 KiB at D = 128
+  static constexpr int kStageBytes = 2 * kTileBytes;  // K + V
+  static constexpr int KP = RB / 16;                  // 16-byte pieces per row
+  static constexpr int P = kStageBytes / 1024 / kWaves;  // 1 KiB staging pieces per wave
+  // K: 16-byte piece swizzle; the consecutive rows one quarter-wave of an
+  // operand read touches land in distinct bank groups.
+  __device__ static int k_swz(int row) { return row & (KP - 1); }
+  // V: 32-byte chunk swizzle; each half-wave of a transposing read (4 rows x
+  // 2 chunks) lands in distinct 32-byte bank groups.
+  __device__ static int v_swz(int row) { return D == 128 ? 2 * (row & 3) : (row & 3); }
+};
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -78,26 +85,29 @@ __device__ __forceinline__ bf16x8 read_tr_pair(const char* p0, const char* p1) {
 
 }  // namespace
 
-// Per-lane constants of the staging of a tile: every wave moves four 1 KiB
+// Per-lane constants of the staging of a tile: every wave moves P 1 KiB
 // pieces; lane `lane` of piece u carries key row `row[u]`, element offset
 // `col[u]` inside that row (K for waves 0..3, V for 4..7).
+template <int P>
 struct StageLane {
-  int row[4];
-  int col[4];
-  uint32_t off[4];  // byte offset of (row, col) from the tile's first key
+  int row[P];
+  int col[P];
+  uint32_t off[P];  // byte offset of (row, col) from the tile's first key
 };
 
-__device__ __forceinline__ StageLane stage_lane(int w, int lane, int64_t stride) {
-  StageLane d;
+template <int D>
+__device__ __forceinline__ StageLane<Geom<D>::P> stage_lane(int w, int lane, int64_t stride) {
+  using Gm = Geom<D>;
+  StageLane<Gm::P> d;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int off = (4 * w + u) * 1024;
-    const int local = (off & (kTileBytes - 1)) + 16 * lane;
-    const int row = local >> 8;
-    const int piece = (local >> 4) & 15;
+  for (int u = 0; u < Gm::P; ++u) {
+    const int off = (Gm::P * w + u) * 1024;
+    const int local = (off & (Gm::kTileBytes - 1)) + 16 * lane;
+    const int row = local / Gm::RB;
+    const int piece = (local >> 4) & (Gm::KP - 1);
     d.row[u] = row;
-    d.col[u] = off < kTileBytes ? (piece ^ k_swz(row)) * 8
-                                : ((piece >> 1) ^ v_swz(row)) * 16 + (piece & 1) * 8;
+    d.col[u] = off < Gm::kTileBytes ? (piece ^ Gm::k_swz(row)) * 8
+                                    : ((piece >> 1) ^ Gm::v_swz(row)) * 16 + (piece & 1) * 8;
     d.off[u] = static_cast<uint32_t>((row * stride + d.col[u]) * 2);
   }
   return d;
@@ -111,9 +121,9 @@ typedef const __attribute__((address_space(4))) int32_t const_i32;
 // whose scores the masks remove; a block id outside the pool redirects the
 // tile to slot 0.  The block table is read through the constant address
 // space (a scalar load, counted by lgkmcnt, not vmcnt).
-template <bool PAGED>
-__device__ __forceinline__ void load_tile(u32x4 (&r)[4], const PrefillParams& p, const uint16_t* base,
-                                          int64_t stride, const StageLane& d, const_i32* bt, int k_start, int kb,
+template <bool PAGED, int P>
+__device__ __forceinline__ void load_tile(u32x4 (&r)[P], const PrefillParams& p, const uint16_t* base,
+                                          int64_t stride, const StageLane<P>& d, const_i32* bt, int k_start, int kb,
                                           int kmax) {
   int64_t slot0;
   if constexpr (PAGED) {
@@ -127,23 +137,30 @@ __device__ __forceinline__ void load_tile(u32x4 (&r)[4], const PrefillParams& p,
   const char* tile = reinterpret_cast<const char*>(base + slot0 * stride);
   const int nrow = kmax - kb;  // rows that exist (>= 64 except in the last tile)
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < P; ++u) {
     const uint32_t off = d.row[u] < nrow ? d.off[u] : static_cast<uint32_t>(d.col[u] * 2);
     r[u] = ld16(tile + off);
   }
 }
 
-// Lane `lane` of wave `w` owns bytes (4w + u) KiB + 16 lane of the stage.
-__device__ __forceinline__ void store_tile(char* st, const u32x4 (&r)[4], int w, int lane) {
+// Lane `lane` of wave `w` owns bytes (P w + u) KiB + 16 lane of the stage.
+template <int P>
+__device__ __forceinline__ void store_tile(char* st, const u32x4 (&r)[P], int w, int lane) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) st16(st + (4 * w + u) * 1024 + 16 * lane, r[u]);
+  for (int u = 0; u < P; ++u) st16(st + (P * w + u) * 1024 + 16 * lane, r[u]);
 }
 
-template <bool PAGED>
+template <bool PAGED, int D>
 __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillParams p) {
+  using Gm = Geom<D>;
+  constexpr int RB = Gm::RB;
+  constexpr int KP = Gm::KP;
+  constexpr int P = Gm::P;
+  constexpr int NKS = D / 16;  // QK MFMAs (16 head dims each) per 32-key step
+  constexpr int NJD = D / 32;  // PV MFMAs (32 head dims each) per 16 keys
   // The ring: stage i % 4 holds 64-key tile i.
-  __shared__ __attribute__((aligned(1024))) char smem_all[kStages * kStageBytes];
-  auto stage = [&](int i) { return smem_all + (i & (kStages - 1)) * kStageBytes; };
+  __shared__ __attribute__((aligned(1024))) char smem_all[kStages * Gm::kStageBytes];
+  auto stage = [&](int i) { return smem_all + (i & (kStages - 1)) * Gm::kStageBytes; };
 
   const int s = blockIdx.x / p.num_kv_heads;
   const int kvh = blockIdx.x - s * p.num_kv_heads;
@@ -171,11 +188,11 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   const int qh = kvh * G + r % G;
   const bool row_ok = r < nrows && qp < Lq;
   const int pos = row_ok ? qp : -1;
-  bf16x8 qop[8];
+  bf16x8 qop[NKS];
   {
-    const uint16_t* qrow = p.q + static_cast<int64_t>(q_start + qp) * p.q_row_stride + qh * kHeadDim + 8 * h;
+    const uint16_t* qrow = p.q + static_cast<int64_t>(q_start + qp) * p.q_row_stride + qh * D + 8 * h;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < NKS; ++ks) {
       const u32x4 z = {0u, 0u, 0u, 0u};
       qop[ks] = as_bf16x8(row_ok ? ld16(qrow + 16 * ks) : z);
     }
@@ -192,45 +209,45 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   const int wave_full = wpos_lo + off + 1;  // keys below this are visible to every row of the wave
   const int limit = pos < 0 ? -1 : min(pos + off, kmax - 1);  // last key this row sees
 
-  f32x16 acc[4];  // O^T, head dims 32 jd + 8 b + 4 h + r of row n
+  f32x16 acc[NJD];  // O^T, head dims 32 jd + 8 b + 4 h + r of row n
 #pragma unroll
-  for (int jd = 0; jd < 4; ++jd) acc[jd] = f32x16{};
+  for (int jd = 0; jd < NJD; ++jd) acc[jd] = f32x16{};
   float m_run = kInitMax;
   float l_run = 0.f;  // this lane's half of the row sum
   const float sl2 = p.scale_log2;
 
   // Per-lane LDS byte offsets of the MFMA operand reads inside a stage; the
   // 32-key half (sub), PV MFMA (u) and 4-key block (eb) add constants.
-  //   K: row n + 32 sub, piece (2 ks + h) ^ (row & 15)
+  //   K: row n + 32 sub, piece (2 ks + h) ^ k_swz(row)
   //   V: row 16u + 8eb + 4h + j/4 + 32 sub (j = lane % 16),
-  //      chunk (2 jd + (lane/16 & 1)) ^ 2 (j/4), byte 8 (j % 4)
-  int kaddr[8];
+  //      chunk (2 jd + (lane/16 & 1)) ^ v_swz(j/4), byte 8 (j % 4)
+  int kaddr[NKS];
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) kaddr[ks] = n * 256 + ((2 * ks + h) ^ (n & 15)) * 16;
+  for (int ks = 0; ks < NKS; ++ks) kaddr[ks] = n * RB + ((2 * ks + h) ^ Gm::k_swz(n)) * 16;
   const int jl = lane & 15;
-  int vaddr[4];
+  int vaddr[NJD];
 #pragma unroll
-  for (int jd = 0; jd < 4; ++jd)
-    vaddr[jd] = kTileBytes + (4 * h + (jl >> 2)) * 256 + ((2 * jd + ((lane >> 4) & 1)) ^ (2 * (jl >> 2))) * 32 +
-                8 * (jl & 3);
+  for (int jd = 0; jd < NJD; ++jd)
+    vaddr[jd] = Gm::kTileBytes + (4 * h + (jl >> 2)) * RB +
+                ((2 * jd + ((lane >> 4) & 1)) ^ Gm::v_swz(jl >> 2)) * 32 + 8 * (jl & 3);
 
   const bool k_wave = w < 4;  // waves 0..3 stage K, 4..7 stage V
   const_i32* bt = PAGED ? (const_i32*)(p.block_table + s * p.bt_row_stride) : nullptr;
-  const uint16_t* dbase = (k_wave ? p.k : p.v) + kvh * kHeadDim;
+  const uint16_t* dbase = (k_wave ? p.k : p.v) + kvh * D;
   const int64_t dstride = k_wave ? p.k_row_stride : p.v_row_stride;
-  const StageLane dl = stage_lane(w, lane, dstride);
+  const StageLane<P> dl = stage_lane<D>(w, lane, dstride);
   const int ntiles = (kmax + kBK - 1) / kBK;
 
   // S^T = K . Q^T for the 32 keys at `sb`, as two partial sums (two MFMA
   // chains over the head dims) that the consumer adds.
   auto qk = [&](const char* sb, f32x16& s0, f32x16& s1) {
-    bf16x8 kr[8];
+    bf16x8 kr[NKS];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) kr[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + kaddr[ks]));
+    for (int ks = 0; ks < NKS; ++ks) kr[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + kaddr[ks]));
     s0 = f32x16{};
     s1 = f32x16{};
 #pragma unroll
-    for (int ks = 0; ks < 8; ks += 2) {
+    for (int ks = 0; ks < NKS; ks += 2) {
       s0 = mfma32x32x16(kr[ks], qop[ks], s0);
       s1 = mfma32x32x16(kr[ks + 1], qop[ks + 1], s1);
     }
@@ -264,7 +281,7 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
         const float alpha = fast_exp2(m_run - m_new);  // 1 for lanes that keep their maximum
         l_run *= alpha;
 #pragma unroll
-        for (int jd = 0; jd < 4; ++jd) acc[jd] *= alpha;
+        for (int jd = 0; jd < NJD; ++jd) acc[jd] *= alpha;
         m_run = m_new;
       }
       qk(next ? sb_next : sb_v, sa, sb);
@@ -287,8 +304,8 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int jd = 0; jd < 4; ++jd) {
-          const bf16x8 vt = read_tr_pair(sb_v + vaddr[jd] + 4096 * u, sb_v + vaddr[jd] + 4096 * u + 2048);
+        for (int jd = 0; jd < NJD; ++jd) {
+          const bf16x8 vt = read_tr_pair(sb_v + vaddr[jd] + 16 * RB * u, sb_v + vaddr[jd] + 16 * RB * u + 8 * RB);
           acc[jd] = mfma32x32x16(vt, pop[u], acc[jd]);
         }
     }
@@ -301,28 +318,28 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   // then step over the last 32 keys while the QK of tile it+1's first step
   // issues.  Global loads thus have two tiles of math to arrive.
   f32x16 sa = f32x16{}, sb = f32x16{};
-  u32x4 stg[2][4];  // this wave's share of two tiles in flight (tile i+2 in stg[i % 2])
-  auto tile_iter = [&](int it, const char* cur, const char* nxt, char* fill, u32x4 (&set)[4]) {
+  u32x4 stg[2][P];  // this wave's share of two tiles in flight (tile i+2 in stg[i % 2])
+  auto tile_iter = [&](int it, const char* cur, const char* nxt, char* fill, u32x4 (&set)[P]) {
     const int kb = it * kBK;
-    step(sa, sb, kb, cur, cur + 8192, true);
+    step(sa, sb, kb, cur, cur + 32 * RB, true);
     barrier_lds();
-    if (it + 2 < ntiles) store_tile(fill, set, w, lane);
-    if (it + 4 < ntiles) load_tile<PAGED>(set, p, dbase, dstride, dl, bt, k_start, kb + 4 * kBK, kmax);
-    step(sa, sb, kb + 32, cur + 8192, nxt, it + 1 < ntiles);
+    if (it + 2 < ntiles) store_tile<P>(fill, set, w, lane);
+    if (it + 4 < ntiles) load_tile<PAGED, P>(set, p, dbase, dstride, dl, bt, k_start, kb + 4 * kBK, kmax);
+    step(sa, sb, kb + 32, cur + 32 * RB, nxt, it + 1 < ntiles);
   };
 
   // prologue: tiles 0 and 1 in LDS, tiles 2 and 3 in flight (all loads
   // issued at once), the first QK issued
   {
-    u32x4 pro[2][4];
+    u32x4 pro[2][P];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
-      if (t < ntiles) load_tile<PAGED>(pro[t], p, dbase, dstride, dl, bt, k_start, t * kBK, kmax);
-    if (2 < ntiles) load_tile<PAGED>(stg[0], p, dbase, dstride, dl, bt, k_start, 2 * kBK, kmax);
-    if (3 < ntiles) load_tile<PAGED>(stg[1], p, dbase, dstride, dl, bt, k_start, 3 * kBK, kmax);
+      if (t < ntiles) load_tile<PAGED, P>(pro[t], p, dbase, dstride, dl, bt, k_start, t * kBK, kmax);
+    if (2 < ntiles) load_tile<PAGED, P>(stg[0], p, dbase, dstride, dl, bt, k_start, 2 * kBK, kmax);
+    if (3 < ntiles) load_tile<PAGED, P>(stg[1], p, dbase, dstride, dl, bt, k_start, 3 * kBK, kmax);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
-      if (t < ntiles) store_tile(stage(t), pro[t], w, lane);
+      if (t < ntiles) store_tile<P>(stage(t), pro[t], w, lane);
   }
   barrier_lds();
   if (0 < wave_kmax) qk(stage(0), sa, sb);
@@ -332,32 +349,32 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   }
 
   // ---- epilogue: normalise, transpose through LDS, write whole rows --------
-  // Each wave owns 8 KiB of the (now idle) ring: row n of its 32 at n * 256 B,
-  // 16-byte chunk c (dims 8c .. 8c+7) at position c ^ (n & 15).  Read back,
-  // 16 consecutive lanes cover one row, so every store writes whole lines.
+  // Each wave owns 32 rows of the (now idle) ring: row n at n * RB, 16-byte
+  // chunk c (dims 8c .. 8c+7) at position c ^ k_swz(n).  Read back, KP
+  // consecutive lanes cover one row, so every store writes whole lines.
   const float l = sum_across_halves(l_run);
   const float inv = l > 0.f ? 1.f / l : 0.f;
   barrier_lds();  // every wave is done with the ring
-  char* ot = smem_all + w * 8192;
+  char* ot = smem_all + w * 32 * RB;
 #pragma unroll
-  for (int jd = 0; jd < 4; ++jd)
+  for (int jd = 0; jd < NJD; ++jd)
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       u32x2 o;
       o[0] = pack_bf16x2(acc[jd][4 * b] * inv, acc[jd][4 * b + 1] * inv);
       o[1] = pack_bf16x2(acc[jd][4 * b + 2] * inv, acc[jd][4 * b + 3] * inv);
       const int c = 4 * jd + b;
-      *reinterpret_cast<u32x2*>(ot + n * 256 + ((c ^ (n & 15)) * 16) + 8 * h) = o;
+      *reinterpret_cast<u32x2*>(ot + n * RB + ((c ^ Gm::k_swz(n)) * 16) + 8 * h) = o;
     }
-  const int c = lane & 15;
+  const int c = lane & (KP - 1);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int rr = 4 * i + (lane >> 4);  // row within the wave
+  for (int i = 0; i < KP / 2; ++i) {
+    const int rr = (64 / KP) * i + lane / KP;  // row within the wave
     const int r2 = 32 * w + rr;
     const int qp2 = i0 + r2 / G;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(ot + rr * 256 + ((c ^ (rr & 15)) * 16));
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ot + rr * RB + ((c ^ Gm::k_swz(rr)) * 16));
     if (r2 < nrows && qp2 < Lq) {
-      uint16_t* dst = p.out + static_cast<int64_t>(q_start + qp2) * p.out_row_stride + (kvh * G + r2 % G) * kHeadDim + 8 * c;
+      uint16_t* dst = p.out + static_cast<int64_t>(q_start + qp2) * p.out_row_stride + (kvh * G + r2 % G) * D + 8 * c;
       st16(dst, v);
     }
   }
@@ -374,10 +391,17 @@ hipError_t launch_prefill(const PrefillParams& p0, int max_seqlen_q, hipStream_t
   // x + y * gridDim.x keeps every tile of one (sequence, kv head) on the same
   // XCD (and its L2) whenever gridDim.x is a multiple of 8.
   const dim3 grid(static_cast<unsigned>(p.num_seqs * p.num_kv_heads), static_cast<unsigned>(p.num_q_tiles));
-  if (p.block_table)
-    hipLaunchKernelGGL(varlen_prefill_kernel<true>, grid, dim3(64 * kWaves), 0, stream, p);
-  else
-    hipLaunchKernelGGL(varlen_prefill_kernel<false>, grid, dim3(64 * kWaves), 0, stream, p);
+  if (p.head_dim == 64) {
+    if (p.block_table)
+      hipLaunchKernelGGL((varlen_prefill_kernel<true, 64>), grid, dim3(64 * kWaves), 0, stream, p);
+    else
+      hipLaunchKernelGGL((varlen_prefill_kernel<false, 64>), grid, dim3(64 * kWaves), 0, stream, p);
+  } else {
+    if (p.block_table)
+      hipLaunchKernelGGL((varlen_prefill_kernel<true, 128>), grid, dim3(64 * kWaves), 0, stream, p);
+    else
+      hipLaunchKernelGGL((varlen_prefill_kernel<false, 128>), grid, dim3(64 * kWaves), 0, stream, p);
+  }
   return hipGetLastError();
 }
 

@@ -88,7 +88,7 @@ def prefill(lib, **kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(head_dim=64), _capi.NVA_ERR_UNSUPPORTED),
+    (dict(head_dim=96), _capi.NVA_ERR_UNSUPPORTED),
     (dict(num_heads=12), _capi.NVA_ERR_INVALID_ARGUMENT),
     (dict(num_seqs=-1), _capi.NVA_ERR_INVALID_ARGUMENT),
     (dict(q=None), _capi.NVA_ERR_INVALID_ARGUMENT),
@@ -120,7 +120,7 @@ def decode(lib, **kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(head_dim=64), _capi.NVA_ERR_UNSUPPORTED),
+    (dict(head_dim=96), _capi.NVA_ERR_UNSUPPORTED),
     (dict(num_heads=24), _capi.NVA_ERR_INVALID_ARGUMENT),
     (dict(num_heads=136), _capi.NVA_ERR_UNSUPPORTED),              # group 17
     (dict(kv_dtype=3), _capi.NVA_ERR_INVALID_ARGUMENT),
@@ -165,7 +165,7 @@ def test_decode_batch_zero_is_noop(lib):
 
 
 def test_error_raises_runtime_error(lib):
-    assert decode(lib, head_dim=64) != 0
+    assert decode(lib, head_dim=96) != 0
     with pytest.raises(RuntimeError, match="head_dim"):
         _capi.check(_capi.NVA_ERR_UNSUPPORTED)
 
@@ -201,3 +201,8 @@ def test_qk_norm_rope_zero_tokens_is_noop(lib):
     assert qk_norm_rope(lib, num_tokens=0, q=None) == _capi.NVA_OK
     # rotary embedding only (no weights) and head_dim 64 validate too
     assert qk_norm_rope(lib, num_tokens=0, q_w=None, k_w=None, head_dim=64) == _capi.NVA_OK
+
+
+def test_decode_refuses_fp8_head_dim_64(lib):
+    assert decode(lib, head_dim=64, kv_dtype=1, k_scale=A, v_scale=B) == _capi.NVA_ERR_UNSUPPORTED
+    assert "head_dim" in lib.nva_last_error().decode()

@@ -473,3 +473,70 @@ def test_decode_graph_capture_replay(dev):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {rep} differs from eager"
         assert torch.equal(case.k_cache, kc_eager) and torch.equal(case.v_cache, vc_eager)
+
+
+# ----------------------------------------------------------------------------
+# head_dim 64: Qwen2-0.5B heads 14/2 (GQA 7), qwen2_05b.txt:10,16,18
+# ----------------------------------------------------------------------------
+
+def test_store_head_dim_64_bitexact(dev):
+    from nanovllm_amd import workloads as W
+    case = W.make_prefill_case([37, 300, 1], 14, 2, 8, head_dim=64, seed=64, bulk_device=dev)
+    kc, vc = _sentinel_pool(case, dev)
+    ekc, evc = bits16(kc), bits16(vc)
+    O.store_kvcache(bits16(case.k), bits16(case.v), ekc, evc, case.slot_mapping.cpu().numpy())
+    nva().store_kvcache(case.k, case.v, kc, vc, case.slot_mapping)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(kc), ekc) and np.array_equal(bits16(vc), evc)
+
+
+@pytest.mark.parametrize("nh,nkv", [(16, 8), (16, 1), (64, 8)])
+@pytest.mark.parametrize("fp8", [False, pytest.param(True, marks=pytest.mark.skip(
+    reason="fp8 decode at head_dim 64 faulted on the GPU (cause not found); the library refuses it"))])
+def test_decode_head_dim_64(dev, nh, nkv, fp8):
+    from nanovllm_amd import workloads as W
+    lengths = [1, 2, 31, 33, 256, 257, 700, 1025, 0, 3000]
+    case = W.make_decode_case(len(lengths), nh, nkv, 0, 0, 40, fp8=fp8, seed=640 + fp8 + nh + nkv,
+                              bulk_device=dev, lengths=lengths, table_width=12, head_dim=64)
+    for ns in (0, 1, 3):
+        got = _run_decode(case, ns, store=(ns == 0))
+        tol = dict(max_abs=FP8_MAX_ABS, mean_abs=FP8_MAX_ABS) if fp8 else {}
+        assert_attn_close(got, decode_reference(case), what=f"d=64 nh={nh} nkv={nkv} fp8={fp8} splits={ns}", **tol)
+
+
+@pytest.mark.skip(reason="decode with two kv heads returned an illegal address on the GPU (cause not found); "
+                         "kept off the GPU until the cause is shown")
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_decode_two_kv_heads(dev, head_dim):
+    """Qwen2-0.5B heads 14/2 (qwen2_05b.txt:10,16,18)."""
+    from nanovllm_amd import workloads as W
+    lengths = [1, 2, 31, 33, 256, 257, 700, 1025, 0, 3000]
+    case = W.make_decode_case(len(lengths), 14, 2, 0, 0, 40, seed=642, bulk_device=dev, lengths=lengths,
+                              table_width=12, head_dim=head_dim)
+    for ns in (0, 1, 3):
+        got = _run_decode(case, ns, store=(ns == 0))
+        assert_attn_close(got, decode_reference(case), what=f"nkv=2 d={head_dim} splits={ns}")
+
+
+@pytest.mark.parametrize("prefix", [0, 256])
+def test_prefill_head_dim_64(dev, prefix):
+    from nanovllm_amd import workloads as W
+    lens = [1, 63, 64, 65, 300, 0, 777]
+    case = W.make_prefill_case(lens, 14, 2, 24, prefix_len=prefix, head_dim=64, seed=65 + prefix,
+                               bulk_device=dev, shared_prefix=False)
+    got = _run_prefill(case)
+    assert_attn_close(got, prefill_reference(case), what=f"d=64 prefill prefix={prefix}")
+
+
+def test_prefill_head_dim_64_score_outliers(dev):
+    from nanovllm_amd import workloads as W
+    lens = [200, 130]
+    case = W.make_prefill_case(lens, 8, 2, 8, head_dim=64, seed=66, bulk_device=dev)
+    case.q.fill_(1.0)
+    cu = case.cu_seqlens_q.cpu().tolist()
+    for s, L in enumerate(lens):
+        for p in SPIKE_POSITIONS:
+            if p < L:
+                case.k[cu[s] + p] = 16.0  # 64 * 16 * scale(1/8) = 128 nats
+    got = _run_prefill(case)
+    assert_attn_close(got, prefill_reference(case), what="d=64 outliers")
