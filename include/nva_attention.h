@@ -9,6 +9,8 @@
  *   nva_decode         <- flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
  *                         cache_seqlens, block_table, softmax_scale,
  *                         causal=True)                             attention.py:74-77
+ * and one fused producer step just before attention:
+ *   nva_qk_norm_rope   <- q_norm / k_norm + rotary_emb             qwen3.py:91-105
  *
  * Conventions shared by every entry point
  *   - Plain pointers to device memory, sizes and strides in ELEMENTS (not bytes).
@@ -37,7 +39,7 @@ extern "C" {
 
 #define NVA_OK 0
 #define NVA_ERR_INVALID_ARGUMENT 1 /* shape, stride, alignment or pointer is wrong */
-#define NVA_ERR_UNSUPPORTED 2      /* valid but not implemented (e.g. head_dim != 128) */
+#define NVA_ERR_UNSUPPORTED 2      /* valid but not implemented (e.g. head_dim 96) */
 #define NVA_ERR_HIP 3              /* the HIP runtime rejected a launch */
 #define NVA_ERR_WORKSPACE 4        /* workspace missing or smaller than required */
 
@@ -84,6 +86,7 @@ int nva_store_kvcache(const void* key, int64_t key_row_stride,
  * Causal masking is bottom-right aligned: query i of a sequence with Lq queries and Lk
  * keys sees keys j <= i + (Lk - Lq).  A query row with no visible key yields zeros.
  * max_seqlen_q bounds the launch grid (host value, graph-capture safe).
+ * head_dim 64 or 128; a paged cache needs block_size % 64 == 0 and bf16.
  */
 int nva_prefill(const void* q, int64_t q_row_stride,
                 const void* k, int64_t k_row_stride,
@@ -115,6 +118,8 @@ int64_t nva_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num
  * max_blocks_per_seq*block_size; a block id outside [0, num_blocks) makes its keys
  * masked; a sequence with no key yields zeros.
  * kv_dtype NVA_DTYPE_FP8_E4M3: caches are e4m3fn with per-kv-head scales k_scale/v_scale.
+ * head_dim 64 or 128 for a bf16 cache; an fp8 cache needs head_dim 128.  GQA group <= 16,
+ * block_size a multiple of 32.
  */
 int nva_decode(const void* q, int64_t q_row_stride,
                const void* k_cache, const void* v_cache, int32_t kv_dtype,
