@@ -57,6 +57,9 @@ struct Geom {
   static constexpr int RB = 2 * D;
   static constexpr int kTileBytes = kBK * RB;        // one K (or V) tile: 16 KiB at D = 128
   static constexpr int kStageBytes = 2 * kTileBytes;  // K + V
+  // K tiles of the ring first, V tiles after them: with the loop unrolled over
+  // the stages every operand read is a per-lane base plus an immediate < 64 KiB.
+  static constexpr int kVRing = kStages * kTileBytes;
   static constexpr int KP = RB / 16;                  // 16-byte pieces per row
   static constexpr int P = kStageBytes / 1024 / kWaves;  // 1 KiB staging pieces per wave
   // K: 16-byte piece swizzle; the consecutive rows one quarter-wave of an
@@ -143,11 +146,13 @@ __device__ __forceinline__ void load_tile(u32x4 (&r)[P], const PrefillParams& p,
   }
 }
 
-// Lane `lane` of wave `w` owns bytes (P w + u) KiB + 16 lane of the stage.
+// Lane `lane` of wave `w` owns bytes (P w + u) KiB + 16 lane of the stage's
+// K tile followed by its V tile; `st` is the stage's K tile and its V tile
+// lies v_skip + tile bytes further on.
 template <int P>
-__device__ __forceinline__ void store_tile(char* st, const u32x4 (&r)[P], int w, int lane) {
+__device__ __forceinline__ void store_tile(char* st, const u32x4 (&r)[P], int w, int lane, int v_skip) {
 #pragma unroll
-  for (int u = 0; u < P; ++u) st16(st + (P * w + u) * 1024 + 16 * lane, r[u]);
+  for (int u = 0; u < P; ++u) st16(st + v_skip + (P * w + u) * 1024 + 16 * lane, r[u]);
 }
 
 template <bool PAGED, int D>
@@ -158,9 +163,10 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   constexpr int P = Gm::P;
   constexpr int NKS = D / 16;  // QK MFMAs (16 head dims each) per 32-key step
   constexpr int NJD = D / 32;  // PV MFMAs (32 head dims each) per 16 keys
-  // The ring: stage i % 4 holds 64-key tile i.
+  // The ring: stage i % 4 holds 64-key tile i, its K at i % 4 * kTileBytes
+  // and its V kVRing further on.
   __shared__ __attribute__((aligned(1024))) char smem_all[kStages * Gm::kStageBytes];
-  auto stage = [&](int i) { return smem_all + (i & (kStages - 1)) * Gm::kStageBytes; };
+  auto stage = [&](int i) { return smem_all + (i & (kStages - 1)) * Gm::kTileBytes; };
 
   const int s = blockIdx.x / p.num_kv_heads;
   const int kvh = blockIdx.x - s * p.num_kv_heads;
@@ -213,7 +219,7 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
 #pragma unroll
   for (int jd = 0; jd < NJD; ++jd) acc[jd] = f32x16{};
   float m_run = kInitMax;
-  float l_run = 0.f;  // this lane's half of the row sum
+  float l_run[2] = {0.f, 0.f};  // this lane's half of the row sum, two dot2 chains
   const float sl2 = p.scale_log2;
 
   // Per-lane LDS byte offsets of the MFMA operand reads inside a stage; the
@@ -228,7 +234,7 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   int vaddr[NJD];
 #pragma unroll
   for (int jd = 0; jd < NJD; ++jd)
-    vaddr[jd] = Gm::kTileBytes + (4 * h + (jl >> 2)) * RB +
+    vaddr[jd] = Gm::kVRing + (4 * h + (jl >> 2)) * RB +
                 ((2 * jd + ((lane >> 4) & 1)) ^ Gm::v_swz(jl >> 2)) * 32 + 8 * (jl & 3);
 
   const bool k_wave = w < 4;  // waves 0..3 stage K, 4..7 stage V
@@ -236,33 +242,27 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   const uint16_t* dbase = (k_wave ? p.k : p.v) + kvh * D;
   const int64_t dstride = k_wave ? p.k_row_stride : p.v_row_stride;
   const StageLane<P> dl = stage_lane<D>(w, lane, dstride);
+  const int v_skip = k_wave ? 0 : Gm::kVRing - Gm::kTileBytes;
   const int ntiles = (kmax + kBK - 1) / kBK;
 
-  // S^T = K . Q^T for the 32 keys at `sb`, as two partial sums (two MFMA
-  // chains over the head dims) that the consumer adds.
-  auto qk = [&](const char* sb, f32x16& s0, f32x16& s1) {
+  // S^T = K . Q^T for the 32 keys at `sb`: one accumulation chain over the
+  // head dims (dependent MFMAs of one shape issue back to back).
+  auto qk = [&](const char* sb, f32x16& sacc) {
     bf16x8 kr[NKS];
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) kr[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + kaddr[ks]));
-    s0 = f32x16{};
-    s1 = f32x16{};
+    sacc = mfma32x32x16(kr[0], qop[0], f32x16{});
 #pragma unroll
-    for (int ks = 0; ks < NKS; ks += 2) {
-      s0 = mfma32x32x16(kr[ks], qop[ks], s0);
-      s1 = mfma32x32x16(kr[ks + 1], qop[ks + 1], s1);
-    }
+    for (int ks = 1; ks < NKS; ++ks) sacc = mfma32x32x16(kr[ks], qop[ks], sacc);
   };
 
-  // One 32-key step: softmax of the scores sa + sb of keys key0 .. key0+31
+  // One 32-key step: softmax of the scores s_cur of keys key0 .. key0+31
   // and O^T += V^T P^T with V from `sb_v`; the QK MFMAs of the following step
   // (keys at `sb_next`) are issued in between, so the matrix pipe works on
   // them while the VALU does the exponentials.  Without a following step they
   // run on `sb_v` and their result is unused, which keeps the block branch-free.
-  auto step = [&](f32x16& sa, f32x16& sb, int key0, const char* sb_v, const char* sb_next, bool next) {
+  auto step = [&](f32x16& sv, f32x16& s_next, int key0, const char* sb_v, const char* sb_next, bool next) {
     if (key0 < wave_kmax) {  // otherwise every key of this step is masked for this wave
-      float sv[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sv[i] = sa[i] + sb[i];
       if (key0 + 32 > wave_full || key0 + 32 > kmax) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -273,31 +273,41 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
       float mx = sv[0];
 #pragma unroll
       for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sv[i]);
-      mx = max_across_halves(mx) * sl2;  // log2 domain (sl2 > 0)
-      // lazy maximum: move it only when a score exceeds it by more than kTau
-      const bool grow = mx > m_run + kTau;
-      if (__builtin_amdgcn_ballot_w64(grow)) {
+      mx *= sl2;  // log2 domain (sl2 > 0)
+      // Lazy maximum, shared by the two lanes holding a row (n and n + 32): it
+      // moves only when a score exceeds it by more than kTau.  Each lane first
+      // checks only its own 16 scores; the cross-lane maximum and the rescale
+      // run only when some lane exceeds it (the first step, rare outliers).
+      if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau)) {
+        mx = max_across_halves(mx);
+        const bool grow = mx > m_run + kTau;  // the same in both lanes of a row
         const float m_new = grow ? mx : m_run;
-        const float alpha = fast_exp2(m_run - m_new);  // 1 for lanes that keep their maximum
-        l_run *= alpha;
+        const float alpha = fast_exp2(m_run - m_new);  // 1 for rows that keep their maximum
+        l_run[0] *= alpha;
+        l_run[1] *= alpha;
 #pragma unroll
         for (int jd = 0; jd < NJD; ++jd) acc[jd] *= alpha;
         m_run = m_new;
       }
-      qk(next ? sb_next : sb_v, sa, sb);
+      qk(next ? sb_next : sb_v, s_next);
       const float mneg = -m_run;
-      float pv[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        pv[i] = fast_exp2(__builtin_fmaf(sv[i], sl2, mneg));
-        l_run += pv[i];
-      }
+      const bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
       bf16x8 pop[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         u32x4 pw;
 #pragma unroll
-        for (int q2 = 0; q2 < 4; ++q2) pw[q2] = pack_bf16x2(pv[8 * u + 2 * q2], pv[8 * u + 2 * q2 + 1]);
+        for (int q2 = 0; q2 < 4; ++q2) {
+          const float a = fast_exp2(__builtin_fmaf(sv[8 * u + 2 * q2], sl2, mneg));
+          const float b = fast_exp2(__builtin_fmaf(sv[8 * u + 2 * q2 + 1], sl2, mneg));
+          // The row sum adds the rounded probabilities the PV product uses,
+          // two at a time (v_dot2 against (1, 1)).  The dot2 takes the bf16
+          // pair itself: this compiler misselects the register when its
+          // operand is a bitcast element of a 4-dword vector.
+          const bf16x2 pb = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+          pw[q2] = __builtin_bit_cast(uint32_t, pb);
+          l_run[q2 & 1] = __builtin_amdgcn_fdot2_f32_bf16(pb, ones, l_run[q2 & 1], false);
+        }
         pop[u] = as_bf16x8(pw);
       }
       // V^T operands: head dims 32 jd .. +31 of PV MFMA u's 16 keys
@@ -317,15 +327,17 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   // into the stage `fill` that tile it-2 left, and load tile it+4 into `set`;
   // then step over the last 32 keys while the QK of tile it+1's first step
   // issues.  Global loads thus have two tiles of math to arrive.
-  f32x16 sa = f32x16{}, sb = f32x16{};
+  // Scores ping-pong between two buffers: the first step of a tile reads s0
+  // and issues the QK of the second into s1, which issues the next tile's into s0.
+  f32x16 s0 = f32x16{}, s1 = f32x16{};
   u32x4 stg[2][P];  // this wave's share of two tiles in flight (tile i+2 in stg[i % 2])
   auto tile_iter = [&](int it, const char* cur, const char* nxt, char* fill, u32x4 (&set)[P]) {
     const int kb = it * kBK;
-    step(sa, sb, kb, cur, cur + 32 * RB, true);
+    step(s0, s1, kb, cur, cur + 32 * RB, true);
     barrier_lds();
-    if (it + 2 < ntiles) store_tile<P>(fill, set, w, lane);
+    if (it + 2 < ntiles) store_tile<P>(fill, set, w, lane, v_skip);
     if (it + 4 < ntiles) load_tile<PAGED, P>(set, p, dbase, dstride, dl, bt, k_start, kb + 4 * kBK, kmax);
-    step(sa, sb, kb + 32, cur + 32 * RB, nxt, it + 1 < ntiles);
+    step(s1, s0, kb + 32, cur + 32 * RB, nxt, it + 1 < ntiles);
   };
 
   // prologue: tiles 0 and 1 in LDS, tiles 2 and 3 in flight (all loads
@@ -339,20 +351,29 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
     if (3 < ntiles) load_tile<PAGED, P>(stg[1], p, dbase, dstride, dl, bt, k_start, 3 * kBK, kmax);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
-      if (t < ntiles) store_tile<P>(stage(t), pro[t], w, lane);
+      if (t < ntiles) store_tile<P>(stage(t), pro[t], w, lane, v_skip);
   }
   barrier_lds();
-  if (0 < wave_kmax) qk(stage(0), sa, sb);
-  for (int it = 0; it < ntiles; it += 2) {
-    tile_iter(it, stage(it), stage(it + 1), stage(it + 2), stg[0]);
-    if (it + 1 < ntiles) tile_iter(it + 1, stage(it + 1), stage(it + 2), stage(it + 3), stg[1]);
+  if (0 < wave_kmax) qk(stage(0), s0);
+  // Use the softmax scale (a kernel-argument scalar load) once here, so its
+  // wait lands in the prologue rather than on the first use inside the loop,
+  // where it would also wait for the LDS reads in flight on every step.
+  asm volatile("" ::"s"(sl2));
+  // unrolled over the ring's stages, so the stage offsets are immediates
+  for (int it0 = 0; it0 < ntiles; it0 += kStages) {
+#pragma unroll
+    for (int t = 0; t < kStages; ++t) {
+      const int it = it0 + t;
+      if (it >= ntiles) break;
+      tile_iter(it, stage(t), stage(t + 1), stage(t + 2), stg[t & 1]);
+    }
   }
 
   // ---- epilogue: normalise, transpose through LDS, write whole rows --------
   // Each wave owns 32 rows of the (now idle) ring: row n at n * RB, 16-byte
   // chunk c (dims 8c .. 8c+7) at position c ^ k_swz(n).  Read back, KP
   // consecutive lanes cover one row, so every store writes whole lines.
-  const float l = sum_across_halves(l_run);
+  const float l = sum_across_halves(l_run[0] + l_run[1]);
   const float inv = l > 0.f ? 1.f / l : 0.f;
   barrier_lds();  // every wave is done with the ring
   char* ot = smem_all + w * 32 * RB;
