@@ -118,26 +118,36 @@ __device__ __forceinline__ StageLane<Geom<D>::P> stage_lane(int w, int lane, int
 
 typedef const __attribute__((address_space(4))) int32_t const_i32;
 
-// Global loads of this wave's quarter-KiB pieces of one 64-key K/V tile into
-// registers (`r`); store_tile later writes them to their swizzled LDS places.
-// Keys at or beyond kmax are redirected to the tile's first key, a valid row
-// whose scores the masks remove; a block id outside the pool redirects the
-// tile to slot 0.  The block table is read through the constant address
-// space (a scalar load, counted by lgkmcnt, not vmcnt).
-template <bool PAGED, int P>
-__device__ __forceinline__ void load_tile(u32x4 (&r)[P], const PrefillParams& p, const uint16_t* base,
-                                          int64_t stride, const StageLane<P>& d, const_i32* bt, int k_start, int kb,
-                                          int kmax) {
+// Block id of the page holding key kb (-1 past the table's width).  The block
+// table is read through the constant address space: a scalar load, counted by
+// lgkmcnt, not vmcnt.
+__device__ __forceinline__ int page_of(const PrefillParams& p, const_i32* bt, int kb) {
+  const int bi = kb / p.block_size;
+  return bi < p.max_blocks ? bt[bi] : -1;
+}
+
+// Address of the first key of the 64-key tile at kb: packed K/V from
+// k_start, or the page `page` (paged caches only; a block id outside the pool
+// redirects the tile to slot 0).
+template <bool PAGED>
+__device__ __forceinline__ const char* tile_base(const PrefillParams& p, const uint16_t* base, int64_t stride, int page,
+                                                 int k_start, int kb) {
   int64_t slot0;
   if constexpr (PAGED) {
-    const int bi = kb / p.block_size;
-    const int page = bi < p.max_blocks ? bt[bi] : -1;
     const bool ok = page >= 0 && page < p.num_blocks;
     slot0 = ok ? static_cast<int64_t>(page) * p.block_size + (kb % p.block_size) : 0;
   } else {
     slot0 = static_cast<int64_t>(k_start) + kb;
   }
-  const char* tile = reinterpret_cast<const char*>(base + slot0 * stride);
+  return reinterpret_cast<const char*>(base + slot0 * stride);
+}
+
+// Global loads of this wave's quarter-KiB pieces of one 64-key K/V tile (at
+// `tile`, key kb) into registers (`r`); store_tile later writes them to their
+// swizzled LDS places.  Keys at or beyond kmax are redirected to the tile's
+// first key, a valid row whose scores the masks remove.
+template <int P>
+__device__ __forceinline__ void load_tile(u32x4 (&r)[P], const char* tile, const StageLane<P>& d, int kb, int kmax) {
   const int nrow = kmax - kb;  // rows that exist (>= 64 except in the last tile)
 #pragma unroll
   for (int u = 0; u < P; ++u) {
@@ -331,24 +341,35 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   // and issues the QK of the second into s1, which issues the next tile's into s0.
   f32x16 s0 = f32x16{}, s1 = f32x16{};
   u32x4 stg[2][P];  // this wave's share of two tiles in flight (tile i+2 in stg[i % 2])
+  // Paged caches: block id of the next tile to load, read one tile ahead so
+  // the scalar load's latency is covered by a tile of math (its wait falls in
+  // the next barrier, which waits for lgkmcnt anyway).
+  int page_ahead = PAGED && 4 < ntiles ? page_of(p, bt, 4 * kBK) : 0;
   auto tile_iter = [&](int it, const char* cur, const char* nxt, char* fill, u32x4 (&set)[P]) {
     const int kb = it * kBK;
     step(s0, s1, kb, cur, cur + 32 * RB, true);
     barrier_lds();
+    // the next load's address first: its page id is the only scalar-load
+    // wait here, and it must not also wait for the LDS stores below
+    const char* tile4 = tile_base<PAGED>(p, dbase, dstride, page_ahead, k_start, kb + 4 * kBK);
     if (it + 2 < ntiles) store_tile<P>(fill, set, w, lane, v_skip);
-    if (it + 4 < ntiles) load_tile<PAGED, P>(set, p, dbase, dstride, dl, bt, k_start, kb + 4 * kBK, kmax);
+    if (it + 4 < ntiles) load_tile<P>(set, tile4, dl, kb + 4 * kBK, kmax);
+    if (PAGED && it + 5 < ntiles) page_ahead = page_of(p, bt, kb + 5 * kBK);
     step(s1, s0, kb + 32, cur + 32 * RB, nxt, it + 1 < ntiles);
   };
 
+  auto first_tile = [&](int t) {
+    return tile_base<PAGED>(p, dbase, dstride, PAGED ? page_of(p, bt, t * kBK) : 0, k_start, t * kBK);
+  };
   // prologue: tiles 0 and 1 in LDS, tiles 2 and 3 in flight (all loads
   // issued at once), the first QK issued
   {
     u32x4 pro[2][P];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
-      if (t < ntiles) load_tile<PAGED, P>(pro[t], p, dbase, dstride, dl, bt, k_start, t * kBK, kmax);
-    if (2 < ntiles) load_tile<PAGED, P>(stg[0], p, dbase, dstride, dl, bt, k_start, 2 * kBK, kmax);
-    if (3 < ntiles) load_tile<PAGED, P>(stg[1], p, dbase, dstride, dl, bt, k_start, 3 * kBK, kmax);
+      if (t < ntiles) load_tile<P>(pro[t], first_tile(t), dl, t * kBK, kmax);
+    if (2 < ntiles) load_tile<P>(stg[0], first_tile(2), dl, 2 * kBK, kmax);
+    if (3 < ntiles) load_tile<P>(stg[1], first_tile(3), dl, 3 * kBK, kmax);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
       if (t < ntiles) store_tile<P>(stage(t), pro[t], w, lane, v_skip);
