@@ -460,16 +460,21 @@ __global__ __launch_bounds__(64 * WAVES) void paged_decode_balanced_kernel(Decod
   }
 }
 
-// Log-sum-exp merge of the partials: one wavefront per (sequence, head), two
-// output columns per lane.  Fixed splits: slots b*num_splits + s for the splits
-// that hold keys.  Balanced: slots b + r for the ranges r that overlap the
-// sequence; a sequence inside one range was written directly and is skipped,
-// an empty one gets zeros.
-__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
-  const int bh = blockIdx.x;
-  const int b = bh / p.num_heads;
-  const int h = bh - b * p.num_heads;
-  const int lane = threadIdx.x;
+// Log-sum-exp merge of the partials: one wavefront per (sequence, head), four
+// heads of one sequence per workgroup, two output columns per lane.  Fixed
+// splits: slots b*num_splits + s for the splits that hold keys.  Balanced:
+// slots b + r for the ranges r that overlap the sequence; a sequence inside
+// one range was written directly and is skipped, an empty one gets zeros.
+// One pass: the loads of up to eight partials are issued together and folded
+// into a running (max, sum, output) online, so the only dependent load before
+// them is the step prefix.
+constexpr int kMergeHeads = 4;  // heads (waves) per merge workgroup
+
+__global__ __launch_bounds__(64 * kMergeHeads) void decode_merge_kernel(DecodeParams p) {
+  const int hgroups = (p.num_heads + kMergeHeads - 1) / kMergeHeads;
+  const int b = blockIdx.x / hgroups;
+  const int h = (blockIdx.x - b * hgroups) * kMergeHeads + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   int64_t first, count;
   bool zero = false;
   if (p.balanced_ranges > 0) {
@@ -491,6 +496,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
     count = (ctx + p.keys_per_split - 1) / p.keys_per_split;
     zero = count == 0;
   }
+  if (h >= p.num_heads) return;
   // A partial slot holds data unless it is a balanced range with no steps (P > T).
   const int64_t T = p.balanced_ranges > 0 ? p.ws_prefix[p.batch] : 0;
   auto has_data = [&](int64_t s) {
@@ -498,35 +504,29 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
     const int64_t rr = first - b + s;
     return range_start(rr, T, p.balanced_ranges) != range_start(rr + 1, T, p.balanced_ranges);
   };
-  // pass 1: the maximum over the partials, lanes in parallel
-  float M = kNegInf;
-  if (!zero)
-    for (int64_t s = lane; s < count; s += 64)
-      if (has_data(s)) M = fmaxf(M, p.ws_ml[((first + s) * p.num_heads + h) * 2]);
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, shfl_xor(M, m));
-  // pass 2: weighted sums, eight partials' loads in flight at a time
   const bool cols = 2 * lane < p.head_dim;  // lane owns output columns 2 lane, 2 lane + 1
-  float L = 0.f, o0 = 0.f, o1 = 0.f;
-  if (!zero && M != kNegInf) {
+  float M = kNegInf, L = 0.f, o0 = 0.f, o1 = 0.f;
+  if (!zero) {
     for (int64_t s0 = 0; s0 < count; s0 += 8) {
-      float w[8], l[8];
-      f32x2 v[8];
+      f32x2 ml[8], v[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int64_t s = s0 + u;
         const bool ok = s < count && has_data(s);
         const int64_t idx = (first + (ok ? s : 0)) * p.num_heads + h;
-        const f32x2 ml = ok ? *reinterpret_cast<const f32x2*>(p.ws_ml + idx * 2) : f32x2{kNegInf, 0.f};
-        w[u] = ok ? fast_exp2(ml[0] - M) : 0.f;
-        l[u] = ml[1];
+        ml[u] = ok ? *reinterpret_cast<const f32x2*>(p.ws_ml + idx * 2) : f32x2{kNegInf, 0.f};
         v[u] = ok && cols ? *reinterpret_cast<const f32x2*>(p.ws_o + idx * p.head_dim + 2 * lane) : f32x2{0.f, 0.f};
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        L += w[u] * l[u];
-        o0 += w[u] * v[u][0];
-        o1 += w[u] * v[u][1];
+        if (ml[u][0] == kNegInf) continue;  // no slot, or no valid key in it
+        const float m_new = fmaxf(M, ml[u][0]);
+        const float a = fast_exp2(M - m_new);  // 0 while M is still -inf
+        const float w = fast_exp2(ml[u][0] - m_new);
+        L = L * a + w * ml[u][1];
+        o0 = o0 * a + w * v[u][0];
+        o1 = o1 * a + w * v[u][1];
+        M = m_new;
       }
     }
   }
@@ -622,8 +622,8 @@ static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
 #undef NVA_LAUNCH_W
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !merge) return e;
-  const dim3 mgrid(static_cast<unsigned>(p.batch * p.num_heads));
-  hipLaunchKernelGGL(decode_merge_kernel, mgrid, dim3(64), 0, stream, p);
+  const dim3 mgrid(static_cast<unsigned>(p.batch * ((p.num_heads + kMergeHeads - 1) / kMergeHeads)));
+  hipLaunchKernelGGL(decode_merge_kernel, mgrid, dim3(64 * kMergeHeads), 0, stream, p);
   return hipGetLastError();
 }
 
