@@ -34,6 +34,8 @@
 // moves only when a score exceeds it by more than kTau (so p <= 2^kTau), which
 // makes the rescale of the accumulators rare.  Masks are evaluated only on
 // tiles that cross the causal diagonal or the key end.
+#include <algorithm>
+
 #include "nva_common.h"
 #include "nva_kernels.h"
 
@@ -165,8 +167,10 @@ __device__ __forceinline__ void store_tile(char* st, const u32x4 (&r)[P], int w,
   for (int u = 0; u < P; ++u) st16(st + v_skip + (P * w + u) * 1024 + 16 * lane, r[u]);
 }
 
+// One work item: query tile `tile` of sequence s, kv head kvh (its GQA group's
+// heads).  `smem_all` is the workgroup's LDS ring; every wave takes part.
 template <bool PAGED, int D>
-__global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillParams p) {
+__device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_all, int s, int kvh, int tile) {
   using Gm = Geom<D>;
   constexpr int RB = Gm::RB;
   constexpr int KP = Gm::KP;
@@ -175,12 +179,8 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   constexpr int NJD = D / 32;  // PV MFMAs (32 head dims each) per 16 keys
   // The ring: stage i % 4 holds 64-key tile i, its K at i % 4 * kTileBytes
   // and its V kVRing further on.
-  __shared__ __attribute__((aligned(1024))) char smem_all[kStages * Gm::kStageBytes];
   auto stage = [&](int i) { return smem_all + (i & (kStages - 1)) * Gm::kTileBytes; };
 
-  const int s = blockIdx.x / p.num_kv_heads;
-  const int kvh = blockIdx.x - s * p.num_kv_heads;
-  const int tile = p.num_q_tiles - 1 - static_cast<int>(blockIdx.y);  // heavy tiles first
   const int q_start = p.cu_q[s];
   const int Lq = p.cu_q[s + 1] - q_start;
   const int k_start = p.cu_k[s];
@@ -191,7 +191,12 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   if (i0 >= Lq) return;
   const int off = Lk - Lq;  // bottom-right causal offset
 
-  const int tid = threadIdx.x;
+  // The thread index passes through an empty asm so that everything derived
+  // from it (operand addresses, staging offsets) is formed per item: hoisted
+  // out of the persistent kernel's item loop, those values would stay live
+  // across items and push the register count past 256.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const int w = tid >> 6;
   const int lane = tid & 63;
   const int n = lane & 31;  // row of this lane within the wave's 32
@@ -422,27 +427,216 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   }
 }
 
+// Direct grid: x = (sequence, kv head), y = query tile, heaviest tiles first.
+// Workgroup id x + y * gridDim.x keeps every tile of one (sequence, kv head)
+// on the same XCD (and its L2) whenever gridDim.x is a multiple of 8.  Tiles
+// past a sequence's end exit at once.  Used when the persistent grid's tables
+// would not fit its LDS.
+template <bool PAGED, int D>
+__global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillParams p) {
+  __shared__ __attribute__((aligned(1024))) char smem_all[kStages * Geom<D>::kStageBytes];
+  const int s = blockIdx.x / p.num_kv_heads;
+  const int kvh = blockIdx.x - s * p.num_kv_heads;
+  const int tile = p.num_q_tiles - 1 - static_cast<int>(blockIdx.y);
+  prefill_item<PAGED, D>(p, smem_all, s, kvh, tile);
+}
+
+// Persistent grid: one workgroup per CU walks the real work items.
+//
+// A grid with one workgroup per (sequence, kv head, query tile) also holds the
+// tiles past the shorter sequences' ends; they exit at once, but a workgroup
+// dispatcher that waits for a particular busy CU then leaves other CUs idle
+// for a whole workgroup's duration (measured: half the CUs idle for the first
+// ~40 us of config 4).  Here every workgroup builds the same table of real
+// items from cu_seqlens_q -- item order: query tile index descending (the
+// heavier tiles first), then sequence, then kv head -- and takes items
+// g, then 2 NW - 1 - g, ... (a snake over the NW workgroups, which balances
+// their totals).  Workgroup g = 8 m + x runs on XCD x, and the snake reverses
+// m only, so one kv head's items stay on one XCD (and its L2) when
+// num_kv_heads is 8.
+constexpr int kPersistMaxSeqs = 1024;
+constexpr int kPersistMaxTiles = 1024;
+constexpr int kThreads = 64 * kWaves;
+
+// Inclusive scan of one value per thread over the workgroup; `total` gets the sum.
+__device__ __forceinline__ int wg_scan_incl(int v, int* s_wsum, int& total) {
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int src = lane >= d ? lane - d : lane;
+    const int t = __builtin_amdgcn_ds_bpermute(src << 2, v);
+    if (lane >= d) v += t;
+  }
+  if (lane == 63) s_wsum[wv] = v;
+  __syncthreads();
+  int before = 0;
+  total = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    const int x = s_wsum[i];
+    before += i < wv ? x : 0;
+    total += x;
+  }
+  __syncthreads();
+  return v + before;
+}
+
+template <bool PAGED, int D>
+__global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(PrefillParams p) {
+  __shared__ __attribute__((aligned(1024))) char smem_all[kStages * Geom<D>::kStageBytes];
+  __shared__ int s_ntq[kPersistMaxSeqs];           // query tiles of each sequence
+  __shared__ int s_start[kPersistMaxTiles + 1];    // first item of each tile level (level T_max: total)
+  __shared__ int s_wsum[kWaves];
+  __shared__ int s_found;
+  const int tid = threadIdx.x;
+  const int S = p.num_seqs;
+  const int T = p.num_q_tiles;
+  const int BP = p.positions_per_tile;
+  const int nkv = p.num_kv_heads;
+
+  // level table: cnt[t] = #{s : ntq_s > t}; items of level t (query tile t of
+  // those sequences, all kv heads) start at s_start[t] = nkv * sum_{t' > t} cnt[t']
+  for (int i = tid; i <= T; i += kThreads) s_start[i] = 0;
+  __syncthreads();
+  for (int i = tid; i < S; i += kThreads) {
+    const int lq = p.cu_q[i + 1] - p.cu_q[i];
+    const int nt = lq > 0 ? min((lq + BP - 1) / BP, T) : 0;
+    s_ntq[i] = nt;
+    if (nt > 0) atomicAdd(&s_start[nt - 1], 1);  // histogram of ntq (bin nt - 1)
+  }
+  __syncthreads();
+  if (tid < 64) {
+    // suffix sums over the levels in chunks of C per lane: first cnt[t] =
+    // sum_{k >= t} hist[k], then start[t] = nkv * sum_{t' > t} cnt[t']
+    const int lane = tid;
+    constexpr int C = kPersistMaxTiles / 64;
+    for (int pass = 0; pass < 2; ++pass) {
+      int local = 0;
+      for (int k = 0; k < C; ++k) {
+        const int t = lane * C + k;
+        local += t < T ? s_start[t] : 0;
+      }
+      // exclusive suffix over lanes (lanes above this one)
+      int suf = local;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int src = lane + d < 64 ? lane + d : lane;
+        const int x = __builtin_amdgcn_ds_bpermute(src << 2, suf);
+        if (lane + d < 64) suf += x;
+      }
+      int acc = suf - local;  // sum over t beyond this lane's chunk
+      for (int k = C - 1; k >= 0; --k) {
+        const int t = lane * C + k;
+        if (t < T) {
+          const int v = s_start[t];
+          if (pass == 0) {
+            acc += v;
+            s_start[t] = acc;  // inclusive: cnt[t]
+          } else {
+            s_start[t] = nkv * acc;  // exclusive: start[t]
+            acc += v;
+          }
+        }
+      }
+      if (pass == 1 && lane == 0) s_start[T] = nkv * (suf);  // total items
+    }
+  }
+  __syncthreads();
+  const int total = s_start[T];
+  const int NW = static_cast<int>(gridDim.x);
+  const int g = static_cast<int>(blockIdx.x);
+  for (int round = 0;; ++round) {
+    int q = g;
+    if (round & 1) q = (NW % 8 == 0) ? 8 * (NW / 8 - 1 - g / 8) + g % 8 : NW - 1 - g;
+    const int64_t item64 = static_cast<int64_t>(round) * NW + q;
+    if (item64 >= total) break;
+    const int item = static_cast<int>(item64);
+    // level t: the smallest t with start[t] <= item (start decreases in t)
+    int lo = 0, hi = T - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (s_start[mid] <= item) hi = mid;
+      else lo = mid + 1;
+    }
+    const int t = lo;
+    const int j = item - s_start[t];
+    int rank = j / nkv;
+    const int kvh = j - rank * nkv;
+    // the rank-th sequence (ascending) with more than t query tiles
+    int seq = -1;
+    for (int c0 = 0; c0 < S; c0 += kThreads) {
+      const int sq = c0 + tid;
+      const int f = sq < S && s_ntq[sq] > t ? 1 : 0;
+      int chunk;
+      const int incl = wg_scan_incl(f, s_wsum, chunk);
+      if (f && incl - 1 == rank) s_found = sq;
+      __syncthreads();
+      if (rank < chunk) {
+        seq = s_found;
+        break;
+      }
+      rank -= chunk;
+    }
+    if (seq < 0) continue;  // not reached with consistent cu_seqlens (uniform over the workgroup)
+    prefill_item<PAGED, D>(p, smem_all, seq, kvh, t);
+    __syncthreads();  // the ring is reused by the next item
+  }
+}
+
 int prefill_positions_per_tile(int group) { return group >= 1 && group <= kRows ? kRows / group : 1; }
+
+// Compute units of the current device (cached per device).
+static int device_cu_count() {
+  static int counts[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (counts[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    counts[dev] = n;
+  }
+  return counts[dev];
+}
 
 hipError_t launch_prefill(const PrefillParams& p0, int max_seqlen_q, hipStream_t stream) {
   if (p0.num_seqs <= 0 || max_seqlen_q <= 0) return hipSuccess;
   PrefillParams p = p0;
   p.positions_per_tile = prefill_positions_per_tile(p.group);
   p.num_q_tiles = (max_seqlen_q + p.positions_per_tile - 1) / p.positions_per_tile;
-  // x: (sequence, kv head) pairs, y: query tiles heaviest first.  Workgroup id
-  // x + y * gridDim.x keeps every tile of one (sequence, kv head) on the same
-  // XCD (and its L2) whenever gridDim.x is a multiple of 8.
+  // Persistent grid when there are enough items to balance; with at most two
+  // per CU its table set-up (one more dependent global load and a few
+  // barriers) costs more than it saves (measured on config 2).
+  const int64_t max_items = static_cast<int64_t>(p.num_seqs) * p.num_kv_heads * p.num_q_tiles;
+  const int cus = device_cu_count();
+  if (p.num_seqs <= kPersistMaxSeqs && p.num_q_tiles <= kPersistMaxTiles && max_items > 2 * int64_t{cus}) {
+    // one workgroup per CU (the ring takes most of a CU's LDS)
+    const unsigned nw = static_cast<unsigned>(cus);
+    const dim3 grid(nw);
+    if (p.head_dim == 64) {
+      if (p.block_table)
+        hipLaunchKernelGGL((varlen_prefill_persistent_kernel<true, 64>), grid, dim3(kThreads), 0, stream, p);
+      else
+        hipLaunchKernelGGL((varlen_prefill_persistent_kernel<false, 64>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+      if (p.block_table)
+        hipLaunchKernelGGL((varlen_prefill_persistent_kernel<true, 128>), grid, dim3(kThreads), 0, stream, p);
+      else
+        hipLaunchKernelGGL((varlen_prefill_persistent_kernel<false, 128>), grid, dim3(kThreads), 0, stream, p);
+    }
+    return hipGetLastError();
+  }
   const dim3 grid(static_cast<unsigned>(p.num_seqs * p.num_kv_heads), static_cast<unsigned>(p.num_q_tiles));
   if (p.head_dim == 64) {
     if (p.block_table)
-      hipLaunchKernelGGL((varlen_prefill_kernel<true, 64>), grid, dim3(64 * kWaves), 0, stream, p);
+      hipLaunchKernelGGL((varlen_prefill_kernel<true, 64>), grid, dim3(kThreads), 0, stream, p);
     else
-      hipLaunchKernelGGL((varlen_prefill_kernel<false, 64>), grid, dim3(64 * kWaves), 0, stream, p);
+      hipLaunchKernelGGL((varlen_prefill_kernel<false, 64>), grid, dim3(kThreads), 0, stream, p);
   } else {
     if (p.block_table)
-      hipLaunchKernelGGL((varlen_prefill_kernel<true, 128>), grid, dim3(64 * kWaves), 0, stream, p);
+      hipLaunchKernelGGL((varlen_prefill_kernel<true, 128>), grid, dim3(kThreads), 0, stream, p);
     else
-      hipLaunchKernelGGL((varlen_prefill_kernel<false, 128>), grid, dim3(64 * kWaves), 0, stream, p);
+      hipLaunchKernelGGL((varlen_prefill_kernel<false, 128>), grid, dim3(kThreads), 0, stream, p);
   }
   return hipGetLastError();
 }

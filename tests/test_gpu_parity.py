@@ -518,6 +518,29 @@ def test_decode_two_kv_heads(dev, head_dim):
         assert_attn_close(got, decode_reference(case), what=f"nkv=2 d={head_dim} splits={ns}")
 
 
+@pytest.mark.parametrize("nh,nkv,d,prefix", [(14, 2, 64, 0), (14, 2, 64, 256), (32, 8, 128, 0), (32, 8, 128, 256)])
+def test_prefill_persistent_many_sequences(dev, nh, nkv, d, prefix):
+    """Enough (sequence, kv head, query tile) items for the persistent grid
+    (more than twice the CU count): ragged lengths with empty query segments
+    (a full prefix hit), one long sequence; every output row vs the oracle."""
+    from nanovllm_amd import workloads as W
+    gen = torch.Generator().manual_seed(900 + nh + d + prefix)
+    S = 40 if d == 64 else 24
+    lens = torch.randint(0, 301 if d == 64 else 401, (S,), generator=gen).tolist()
+    lens[3] = 0
+    lens[7] = 0
+    lens[S - 2] = 1000
+    bs = 256
+    pages = sum(-(-(prefix + x) // bs) for x in lens) + 4
+    case = W.make_prefill_case(lens, nh, nkv, pages, prefix_len=prefix, head_dim=d, seed=901 + nh,
+                               bulk_device=dev, shared_prefix=False)
+    G = nh // nkv
+    bp = 256 // G
+    assert S * nkv * -(-max(lens) // bp) > 2 * 256  # the persistent grid serves this call
+    got = _run_prefill(case)
+    assert_attn_close(got, prefill_reference(case), what=f"persistent prefill nh={nh} nkv={nkv} d={d} prefix={prefix}")
+
+
 @pytest.mark.parametrize("prefix", [0, 256])
 def test_prefill_head_dim_64(dev, prefix):
     from nanovllm_amd import workloads as W
