@@ -10,16 +10,16 @@
 // 64-key tiles held in a 4-stage LDS ring:
 //   K [64 keys][256 B]  16-byte pieces XOR-swizzled by key row (row & 15)
 //   V [64 keys][256 B]  32-byte chunks XOR-swizzled by key row (2 * (row & 3))
-// Every lane stages 16-byte pieces: it loads them from global memory into
-// registers two tiles ahead and writes them to LDS at 16 * lane inside its
+// Tiles are copied global -> LDS by global_load_lds_dwordx4 (no registers),
+// two tiles ahead: every lane moves 16-byte pieces to 16 * lane inside its
 // wave's KiB, so the swizzles are made by choosing each lane's source address.
-// (Global->LDS DMA, global_load_lds_dwordx4, measured slower here.)  One
-// barrier per tile, placed between the tile's two 32-key steps.
+// One barrier per tile, placed between the tile's two 32-key steps.
 //
 // Per 32-key step a wave computes the 32 keys x 32 rows tile S^T = K . Q^T with
-// 32x32x16 bf16 MFMAs (two accumulation chains over the head dim), and the
-// MFMAs of the next step's S^T are issued between the exponentials of the
-// current one, so the matrix pipe and the VALU overlap.  Lane l owns
+// one chain of 32x32x16 bf16 MFMAs over the head dim, and the MFMAs of the
+// next step's S^T (their K operands read at the start of the step) are issued
+// between the exponentials of the current one, so the matrix pipe and the VALU
+// overlap.  Lane l owns
 // row l % 32 and keys 8b + 4h + r (h = l / 32, b, r = 0..3) of the step, so
 // the row maximum needs one permlane32 swap, and the probabilities of
 // registers 8u .. 8u+7 are exactly the P^T operand of PV MFMA u (keys
@@ -144,27 +144,46 @@ __device__ __forceinline__ const char* tile_base(const PrefillParams& p, const u
   return reinterpret_cast<const char*>(base + slot0 * stride);
 }
 
-// Global loads of this wave's quarter-KiB pieces of one 64-key K/V tile (at
-// `tile`, key kb) into registers (`r`); store_tile later writes them to their
-// swizzled LDS places.  Keys at or beyond kmax are redirected to the tile's
-// first key, a valid row whose scores the masks remove.
-template <int P>
-__device__ __forceinline__ void load_tile(u32x4 (&r)[P], const char* tile, const StageLane<P>& d, int kb, int kmax) {
-  const int nrow = kmax - kb;  // rows that exist (>= 64 except in the last tile)
-#pragma unroll
-  for (int u = 0; u < P; ++u) {
-    const uint32_t off = d.row[u] < nrow ? d.off[u] : static_cast<uint32_t>(d.col[u] * 2);
-    r[u] = ld16(tile + off);
-  }
+typedef __attribute__((address_space(3))) char lds_char;
+
+// LDS byte address of a pointer into the workgroup's shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const char* ptr) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_char*)ptr));
 }
 
-// Lane `lane` of wave `w` owns bytes (P w + u) KiB + 16 lane of the stage's
-// K tile followed by its V tile; `st` is the stage's K tile and its V tile
-// lies v_skip + tile bytes further on.
+// Copy 16 bytes per lane from base + off (base uniform, in SGPRs) straight into
+// LDS at lds + 16 * lane (global_load_lds_dwordx4).  Inline asm, so that the
+// compiler sees no LDS store it would have to order against the operand reads
+// of other stages; ordering comes from wait_vmem and the barriers instead.
+__device__ __forceinline__ void dma16(const char* base, uint32_t off, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+
+// Wait until at most N of this wave's vector-memory operations are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Copy this wave's P KiB of one 64-key K/V tile (at `tile`, key kb) into the
+// stage whose K tile is at `st` (its V tile v_skip + tile bytes further on):
+// lane `lane` of piece u lands at (P w + u) KiB + 16 lane and carries the
+// swizzled (row, col) of StageLane.  Keys at or beyond kmax (only in the last
+// tile) are redirected to the tile's first key, a valid row whose scores the
+// masks remove.
 template <int P>
-__device__ __forceinline__ void store_tile(char* st, const u32x4 (&r)[P], int w, int lane, int v_skip) {
+__device__ __forceinline__ void dma_tile(char* st, const char* tile, const StageLane<P>& d, int kb, int kmax, int w,
+                                         int v_skip) {
+  const uint32_t dst = lds_addr(st) + v_skip + P * w * 1024;
+  if (kb + kBK <= kmax) {
 #pragma unroll
-  for (int u = 0; u < P; ++u) st16(st + v_skip + (P * w + u) * 1024 + 16 * lane, r[u]);
+    for (int u = 0; u < P; ++u) dma16(tile, d.off[u], dst + u * 1024);
+  } else {
+    const int nrow = kmax - kb;
+#pragma unroll
+    for (int u = 0; u < P; ++u)
+      dma16(tile, d.row[u] < nrow ? d.off[u] : static_cast<uint32_t>(d.col[u] * 2), dst + u * 1024);
+  }
 }
 
 // One work item: query tile `tile` of sequence s, kv head kvh (its GQA group's
@@ -197,7 +216,7 @@ __device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_
   // across items and push the register count past 256.
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: staging bases stay scalar
   const int lane = tid & 63;
   const int n = lane & 31;  // row of this lane within the wave's 32
   const int h = lane >> 5;  // lane half
@@ -262,13 +281,19 @@ __device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_
 
   // S^T = K . Q^T for the 32 keys at `sb`: one accumulation chain over the
   // head dims (dependent MFMAs of one shape issue back to back).
-  auto qk = [&](const char* sb, f32x16& sacc) {
-    bf16x8 kr[NKS];
+  auto k_read = [&](const char* sb, bf16x8 (&kr)[NKS]) {
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) kr[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + kaddr[ks]));
+  };
+  auto qk_mfma = [&](const bf16x8 (&kr)[NKS], f32x16& sacc) {
     sacc = mfma32x32x16(kr[0], qop[0], f32x16{});
 #pragma unroll
     for (int ks = 1; ks < NKS; ++ks) sacc = mfma32x32x16(kr[ks], qop[ks], sacc);
+  };
+  auto qk = [&](const char* sb, f32x16& sacc) {
+    bf16x8 kr[NKS];
+    k_read(sb, kr);
+    qk_mfma(kr, sacc);
   };
 
   // One 32-key step: softmax of the scores s_cur of keys key0 .. key0+31
@@ -278,6 +303,10 @@ __device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_
   // run on `sb_v` and their result is unused, which keeps the block branch-free.
   auto step = [&](f32x16& sv, f32x16& s_next, int key0, const char* sb_v, const char* sb_next, bool next) {
     if (key0 < wave_kmax) {  // otherwise every key of this step is masked for this wave
+      // K operands of the following QK, read first so that they have landed
+      // by the time its MFMAs issue between the exponentials
+      bf16x8 kr[NKS];
+      k_read(next ? sb_next : sb_v, kr);
       if (key0 + 32 > wave_full || key0 + 32 > kmax) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -304,7 +333,7 @@ __device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_
         for (int jd = 0; jd < NJD; ++jd) acc[jd] *= alpha;
         m_run = m_new;
       }
-      qk(next ? sb_next : sb_v, s_next);
+      qk_mfma(kr, s_next);
       const float mneg = -m_run;
       const bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
       bf16x8 pop[2];
@@ -337,49 +366,51 @@ __device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_
   };
 
   // Tile `it` (in stage `cur`, tile it+1 in `nxt`): step over its first 32
-  // keys; synchronise, after which every wave is done with tile it-1 and
-  // tile it+1 is visible; write tile it+2 (loaded two tiles ago, in `set`)
-  // into the stage `fill` that tile it-2 left, and load tile it+4 into `set`;
-  // then step over the last 32 keys while the QK of tile it+1's first step
-  // issues.  Global loads thus have two tiles of math to arrive.
+  // keys; wait for this wave's copy of tile it+1 (issued two tiles ago) and
+  // synchronise, after which every wave is done with tile it-1 and tile it+1
+  // is visible; start the copy of tile it+3 into the stage `fill` that tile
+  // it-1 left; then step over the last 32 keys while the QK of tile it+1's
+  // first step issues.  Copies thus have two tiles of math to land.
   // Scores ping-pong between two buffers: the first step of a tile reads s0
   // and issues the QK of the second into s1, which issues the next tile's into s0.
   f32x16 s0 = f32x16{}, s1 = f32x16{};
-  u32x4 stg[2][P];  // this wave's share of two tiles in flight (tile i+2 in stg[i % 2])
-  // Paged caches: block id of the next tile to load, read one tile ahead so
+  // Paged caches: block id of the next tile to copy, read one tile ahead so
   // the scalar load's latency is covered by a tile of math (its wait falls in
   // the next barrier, which waits for lgkmcnt anyway).
-  int page_ahead = PAGED && 4 < ntiles ? page_of(p, bt, 4 * kBK) : 0;
-  auto tile_iter = [&](int it, const char* cur, const char* nxt, char* fill, u32x4 (&set)[P]) {
+  int page_ahead = PAGED && 3 < ntiles ? page_of(p, bt, 3 * kBK) : 0;
+  auto tile_iter = [&](int it, const char* cur, const char* nxt, char* fill) {
     const int kb = it * kBK;
     step(s0, s1, kb, cur, cur + 32 * RB, true);
+    if (it + 2 < ntiles)
+      wait_vmem<P>();  // tile it+2's copy may stay in flight
+    else
+      wait_vmem<0>();
     barrier_lds();
-    // the next load's address first: its page id is the only scalar-load
-    // wait here, and it must not also wait for the LDS stores below
-    const char* tile4 = tile_base<PAGED>(p, dbase, dstride, page_ahead, k_start, kb + 4 * kBK);
-    if (it + 2 < ntiles) store_tile<P>(fill, set, w, lane, v_skip);
-    if (it + 4 < ntiles) load_tile<P>(set, tile4, dl, kb + 4 * kBK, kmax);
-    if (PAGED && it + 5 < ntiles) page_ahead = page_of(p, bt, kb + 5 * kBK);
+    if (it + 3 < ntiles)
+      dma_tile<P>(fill, tile_base<PAGED>(p, dbase, dstride, page_ahead, k_start, kb + 3 * kBK), dl, kb + 3 * kBK, kmax,
+                  w, v_skip);
+    if (PAGED && it + 4 < ntiles) page_ahead = page_of(p, bt, kb + 4 * kBK);
     step(s1, s0, kb + 32, cur + 32 * RB, nxt, it + 1 < ntiles);
   };
 
   auto first_tile = [&](int t) {
     return tile_base<PAGED>(p, dbase, dstride, PAGED ? page_of(p, bt, t * kBK) : 0, k_start, t * kBK);
   };
-  // prologue: tiles 0 and 1 in LDS, tiles 2 and 3 in flight (all loads
-  // issued at once), the first QK issued
-  {
-    u32x4 pro[2][P];
+  // prologue: tiles 0 and 1 copied and visible, tile 2's copy started after
+  // the barrier, the first QK issued
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-      if (t < ntiles) load_tile<P>(pro[t], first_tile(t), dl, t * kBK, kmax);
-    if (2 < ntiles) load_tile<P>(stg[0], first_tile(2), dl, 2 * kBK, kmax);
-    if (3 < ntiles) load_tile<P>(stg[1], first_tile(3), dl, 3 * kBK, kmax);
+  for (int t = 0; t < 2; ++t)
+    if (t < ntiles) dma_tile<P>(stage(t), first_tile(t), dl, t * kBK, kmax, w, v_skip);
+  wait_vmem<0>();
+  // An unconditional use of the Q operands: the compiler's own wait for their
+  // loads lands here.  Its only other use before the loop is conditional, and
+  // the compiler would then keep those loads pending into the loop and wait
+  // for all vector memory there -- which, unknown to it, also drains the tile
+  // copies in flight -- on every step.
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-      if (t < ntiles) store_tile<P>(stage(t), pro[t], w, lane, v_skip);
-  }
+  for (int ks = 0; ks < NKS; ++ks) asm volatile("" ::"v"(qop[ks]));
   barrier_lds();
+  if (2 < ntiles) dma_tile<P>(stage(2), first_tile(2), dl, 2 * kBK, kmax, w, v_skip);
   if (0 < wave_kmax) qk(stage(0), s0);
   // Use the softmax scale (a kernel-argument scalar load) once here, so its
   // wait lands in the prologue rather than on the first use inside the loop,
@@ -391,7 +422,7 @@ __device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_
     for (int t = 0; t < kStages; ++t) {
       const int it = it0 + t;
       if (it >= ntiles) break;
-      tile_iter(it, stage(t), stage(t + 1), stage(t + 2), stg[t & 1]);
+      tile_iter(it, stage(t), stage(t + 1), stage(t + 3));
     }
   }
 
