@@ -186,10 +186,117 @@ __device__ __forceinline__ void dma_tile(char* st, const char* tile, const Stage
   }
 }
 
-// One work item: query tile `tile` of sequence s, kv head kvh (its GQA group's
-// heads).  `smem_all` is the workgroup's LDS ring; every wave takes part.
+// A work item -- query tile `tile` of sequence s, kv head kvh (its GQA
+// group's heads) -- with the per-item scalars read from cu_seqlens.
+struct ItemDesc {
+  int s, kvh, tile;
+  int q_start, Lq, k_start, Lk;
+  int i0;      // first query position of the tile
+  int kmax;    // keys [0, kmax) are visible to some row of the tile
+  int ntiles;  // 64-key tiles spanning [0, kmax)
+  bool valid;  // false: no item (s < 0) or a tile past the sequence's end
+};
+
+__device__ __forceinline__ ItemDesc item_desc(const PrefillParams& p, int s, int kvh, int tile) {
+  ItemDesc d{};
+  d.s = s;
+  d.kvh = kvh;
+  d.tile = tile;
+  d.valid = false;
+  if (s < 0) return d;
+  d.q_start = p.cu_q[s];
+  d.Lq = p.cu_q[s + 1] - d.q_start;
+  d.k_start = p.cu_k[s];
+  d.Lk = p.cu_k[s + 1] - d.k_start;
+  d.i0 = tile * p.positions_per_tile;
+  d.valid = d.i0 < d.Lq;
+  const int last_pos = min(d.i0 + p.positions_per_tile, d.Lq) - 1;
+  d.kmax = max(0, min(d.Lk, last_pos + (d.Lk - d.Lq) + 1));
+  d.ntiles = (d.kmax + kBK - 1) / kBK;
+  return d;
+}
+
+// The thread index passes through an empty asm so that everything derived
+// from it (operand addresses, staging offsets) is formed where it is used:
+// hoisted out of the persistent kernel's item loop, those values would stay
+// live across items and push the register count past 256.
+__device__ __forceinline__ int laundered_tid() {
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  return tid;
+}
+
+// Q^T operand of item `it` for this lane: row r = 32w + n, head dims
+// 16 ks + 8h .. +7 for MFMA step ks (zeros for padding rows).
+template <int D>
+__device__ __forceinline__ void item_fetch_q(const PrefillParams& p, const ItemDesc& it, bf16x8 (&qop)[D / 16]) {
+  const int tid = laundered_tid();
+  const int w = tid >> 6;
+  const int lane = tid & 63;
+  const int n = lane & 31;
+  const int h = lane >> 5;
+  const int G = p.group;
+  const int r = kRowsPerWave * w + n;
+  const int qp = it.i0 + r / G;
+  const int qh = it.kvh * G + r % G;
+  const bool row_ok = r < p.positions_per_tile * G && qp < it.Lq;
+  const uint16_t* qrow = p.q + static_cast<int64_t>(it.q_start + qp) * p.q_row_stride + qh * D + 8 * h;
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    qop[ks] = as_bf16x8(row_ok ? ld16(qrow + 16 * ks) : z);
+  }
+}
+
+// Per-wave staging constants of item `it`'s K/V tiles (waves 0..3 copy K,
+// 4..7 copy V).
 template <bool PAGED, int D>
-__device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_all, int s, int kvh, int tile) {
+struct ItemStaging {
+  const_i32* bt;
+  const uint16_t* dbase;
+  int64_t dstride;
+  StageLane<Geom<D>::P> dl;
+  int v_skip;
+  int w;
+
+  __device__ __forceinline__ ItemStaging(const PrefillParams& p, const ItemDesc& it) {
+    using Gm = Geom<D>;
+    const int tid = laundered_tid();
+    w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: staging bases stay scalar
+    const bool k_wave = w < 4;
+    bt = PAGED ? (const_i32*)(p.block_table + static_cast<int64_t>(it.s) * p.bt_row_stride) : nullptr;
+    dbase = (k_wave ? p.k : p.v) + it.kvh * D;
+    dstride = k_wave ? p.k_row_stride : p.v_row_stride;
+    dl = stage_lane<D>(w, tid & 63, dstride);
+    v_skip = k_wave ? 0 : Gm::kVRing - Gm::kTileBytes;
+  }
+  // first key of tile t in global memory
+  __device__ __forceinline__ const char* tile(const PrefillParams& p, const ItemDesc& it, int page, int t) const {
+    return tile_base<PAGED>(p, dbase, dstride, page, it.k_start, t * kBK);
+  }
+  __device__ __forceinline__ void copy(const PrefillParams& p, const ItemDesc& it, char* st, int page, int t) const {
+    dma_tile<Geom<D>::P>(st, tile(p, it, page, t), dl, t * kBK, it.kmax, w, v_skip);
+  }
+};
+
+// Start the copies of item `it`'s tiles 0 and 1 into ring stages 0 and 1.
+template <bool PAGED, int D>
+__device__ __forceinline__ void item_fetch_tiles(const PrefillParams& p, char* smem_all, const ItemDesc& it) {
+  const ItemStaging<PAGED, D> st(p, it);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+    if (t < it.ntiles) st.copy(p, it, smem_all + t * Geom<D>::kTileBytes, PAGED ? page_of(p, st.bt, t * kBK) : 0, t);
+}
+
+// Run work item `it` on the whole workgroup.  Its Q operands (qop) and the
+// copies of its tiles 0 and 1 were issued before (item_fetch_q,
+// item_fetch_tiles).  When `next` is valid, this issues next's Q loads into
+// qop once the last QK has been issued and next's first two tile copies right
+// after the epilogue's barrier, so their latency overlaps the epilogue; the
+// epilogue's transpose therefore uses ring stages 2 and 3 only.
+template <bool PAGED, int D>
+__device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_all, const ItemDesc& item,
+                                            bf16x8 (&qop)[D / 16], const ItemDesc& next) {
   using Gm = Geom<D>;
   constexpr int RB = Gm::RB;
   constexpr int KP = Gm::KP;
@@ -200,46 +307,29 @@ __device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_
   // and its V kVRing further on.
   auto stage = [&](int i) { return smem_all + (i & (kStages - 1)) * Gm::kTileBytes; };
 
-  const int q_start = p.cu_q[s];
-  const int Lq = p.cu_q[s + 1] - q_start;
-  const int k_start = p.cu_k[s];
-  const int Lk = p.cu_k[s + 1] - k_start;
+  const int s = item.s;
+  const int q_start = item.q_start;
+  const int Lq = item.Lq;
+  const int k_start = item.k_start;
+  const int kvh = item.kvh;
   const int G = p.group;
   const int BP = p.positions_per_tile;  // query positions per workgroup (BP * G <= kRows)
-  const int i0 = tile * BP;
-  if (i0 >= Lq) return;
-  const int off = Lk - Lq;  // bottom-right causal offset
+  const int i0 = item.i0;
+  const int off = item.Lk - Lq;  // bottom-right causal offset
+  const int kmax = item.kmax;
+  const int ntiles = item.ntiles;
 
-  // The thread index passes through an empty asm so that everything derived
-  // from it (operand addresses, staging offsets) is formed per item: hoisted
-  // out of the persistent kernel's item loop, those values would stay live
-  // across items and push the register count past 256.
-  int tid = threadIdx.x;
-  asm volatile("" : "+v"(tid));
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: staging bases stay scalar
+  const int tid = laundered_tid();
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int n = lane & 31;  // row of this lane within the wave's 32
   const int h = lane >> 5;  // lane half
   const int nrows = BP * G;
-
-  // Q^T operand: row r = 32w + n, head dims 16 ks + 8h .. +7 for MFMA step ks.
   const int r = kRowsPerWave * w + n;
   const int qp = i0 + r / G;
-  const int qh = kvh * G + r % G;
   const bool row_ok = r < nrows && qp < Lq;
   const int pos = row_ok ? qp : -1;
-  bf16x8 qop[NKS];
-  {
-    const uint16_t* qrow = p.q + static_cast<int64_t>(q_start + qp) * p.q_row_stride + qh * D + 8 * h;
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      qop[ks] = as_bf16x8(row_ok ? ld16(qrow + 16 * ks) : z);
-    }
-  }
 
-  const int last_pos = min(i0 + BP, Lq) - 1;
-  const int kmax = max(0, min(Lk, last_pos + off + 1));  // keys [0, kmax) are visible to some row
   const int w_first = kRowsPerWave * w;
   const int w_last = min(kRowsPerWave * w + kRowsPerWave, nrows) - 1;
   // positions spanned by this wave's rows (empty when the wave holds only padding)
@@ -271,13 +361,10 @@ __device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_
     vaddr[jd] = Gm::kVRing + (4 * h + (jl >> 2)) * RB +
                 ((2 * jd + ((lane >> 4) & 1)) ^ Gm::v_swz(jl >> 2)) * 32 + 8 * (jl & 3);
 
-  const bool k_wave = w < 4;  // waves 0..3 stage K, 4..7 stage V
-  const_i32* bt = PAGED ? (const_i32*)(p.block_table + s * p.bt_row_stride) : nullptr;
-  const uint16_t* dbase = (k_wave ? p.k : p.v) + kvh * D;
-  const int64_t dstride = k_wave ? p.k_row_stride : p.v_row_stride;
-  const StageLane<P> dl = stage_lane<D>(w, lane, dstride);
-  const int v_skip = k_wave ? 0 : Gm::kVRing - Gm::kTileBytes;
-  const int ntiles = (kmax + kBK - 1) / kBK;
+  const ItemStaging<PAGED, D> stg(p, item);
+  (void)s;
+  (void)k_start;
+  (void)kvh;
 
   // S^T = K . Q^T for the 32 keys at `sb`: one accumulation chain over the
   // head dims (dependent MFMAs of one shape issue back to back).
@@ -377,7 +464,7 @@ __device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_
   // Paged caches: block id of the next tile to copy, read one tile ahead so
   // the scalar load's latency is covered by a tile of math (its wait falls in
   // the next barrier, which waits for lgkmcnt anyway).
-  int page_ahead = PAGED && 3 < ntiles ? page_of(p, bt, 3 * kBK) : 0;
+  int page_ahead = PAGED && 3 < ntiles ? page_of(p, stg.bt, 3 * kBK) : 0;
   auto tile_iter = [&](int it, const char* cur, const char* nxt, char* fill) {
     const int kb = it * kBK;
     step(s0, s1, kb, cur, cur + 32 * RB, true);
@@ -386,21 +473,14 @@ __device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_
     else
       wait_vmem<0>();
     barrier_lds();
-    if (it + 3 < ntiles)
-      dma_tile<P>(fill, tile_base<PAGED>(p, dbase, dstride, page_ahead, k_start, kb + 3 * kBK), dl, kb + 3 * kBK, kmax,
-                  w, v_skip);
-    if (PAGED && it + 4 < ntiles) page_ahead = page_of(p, bt, kb + 4 * kBK);
+    if (it + 3 < ntiles) stg.copy(p, item, fill, page_ahead, it + 3);
+    if (PAGED && it + 4 < ntiles) page_ahead = page_of(p, stg.bt, kb + 4 * kBK);
     step(s1, s0, kb + 32, cur + 32 * RB, nxt, it + 1 < ntiles);
   };
 
-  auto first_tile = [&](int t) {
-    return tile_base<PAGED>(p, dbase, dstride, PAGED ? page_of(p, bt, t * kBK) : 0, k_start, t * kBK);
-  };
-  // prologue: tiles 0 and 1 copied and visible, tile 2's copy started after
-  // the barrier, the first QK issued
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-    if (t < ntiles) dma_tile<P>(stage(t), first_tile(t), dl, t * kBK, kmax, w, v_skip);
+  // prologue: tiles 0 and 1 (copies issued before this call) and the Q
+  // operands landed and visible; tile 2's copy starts after the barrier; the
+  // first QK is issued
   wait_vmem<0>();
   // An unconditional use of the Q operands: the compiler's own wait for their
   // loads lands here.  Its only other use before the loop is conditional, and
@@ -410,7 +490,7 @@ __device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks) asm volatile("" ::"v"(qop[ks]));
   barrier_lds();
-  if (2 < ntiles) dma_tile<P>(stage(2), first_tile(2), dl, 2 * kBK, kmax, w, v_skip);
+  if (2 < ntiles) stg.copy(p, item, stage(2), PAGED ? page_of(p, stg.bt, 2 * kBK) : 0, 2);
   if (0 < wave_kmax) qk(stage(0), s0);
   // Use the softmax scale (a kernel-argument scalar load) once here, so its
   // wait lands in the prologue rather than on the first use inside the loop,
@@ -427,13 +507,20 @@ __device__ __forceinline__ void prefill_item(const PrefillParams& p, char* smem_
   }
 
   // ---- epilogue: normalise, transpose through LDS, write whole rows --------
-  // Each wave owns 32 rows of the (now idle) ring: row n at n * RB, 16-byte
-  // chunk c (dims 8c .. 8c+7) at position c ^ k_swz(n).  Read back, KP
-  // consecutive lanes cover one row, so every store writes whole lines.
+  // The next item's Q operands first: the last QK has been issued, so qop is
+  // free, and the loads have the epilogue to land.
+  if (next.valid) item_fetch_q<D>(p, next, qop);
   const float l = sum_across_halves(l_run[0] + l_run[1]);
   const float inv = l > 0.f ? 1.f / l : 0.f;
   barrier_lds();  // every wave is done with the ring
-  char* ot = smem_all + w * 32 * RB;
+  // stages 0 and 1 take the next item's first tiles
+  if (next.valid) item_fetch_tiles<PAGED, D>(p, smem_all, next);
+  // Each wave owns 32 rows in ring stages 2 and 3 (waves 0..3 in the K half,
+  // 4..7 in the V half, two waves per tile): row n at n * RB, 16-byte chunk c
+  // (dims 8c .. 8c+7) at position c ^ k_swz(n).  Read back, KP consecutive
+  // lanes cover one row, so every store writes whole lines.
+  static_assert(2 * kRowsPerWave == kBK, "two waves' rows fill one tile");
+  char* ot = smem_all + (w >> 2) * Gm::kVRing + (2 + ((w >> 1) & 1)) * Gm::kTileBytes + (w & 1) * kRowsPerWave * RB;
 #pragma unroll
   for (int jd = 0; jd < NJD; ++jd)
 #pragma unroll
@@ -469,7 +556,14 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   const int s = blockIdx.x / p.num_kv_heads;
   const int kvh = blockIdx.x - s * p.num_kv_heads;
   const int tile = p.num_q_tiles - 1 - static_cast<int>(blockIdx.y);
-  prefill_item<PAGED, D>(p, smem_all, s, kvh, tile);
+  const ItemDesc it = item_desc(p, s, kvh, tile);
+  if (!it.valid) return;
+  bf16x8 qop[D / 16];
+  item_fetch_q<D>(p, it, qop);
+  item_fetch_tiles<PAGED, D>(p, smem_all, it);
+  ItemDesc none{};
+  none.valid = false;
+  prefill_run<PAGED, D>(p, smem_all, it, qop, none);
 }
 
 // Persistent grid: one workgroup per CU walks the real work items.
@@ -489,28 +583,25 @@ constexpr int kPersistMaxSeqs = 1024;
 constexpr int kPersistMaxTiles = 1024;
 constexpr int kThreads = 64 * kWaves;
 
-// Inclusive scan of one value per thread over the workgroup; `total` gets the sum.
-__device__ __forceinline__ int wg_scan_incl(int v, int* s_wsum, int& total) {
+// The rank-th sequence (ascending, 0-based) with more than t query tiles, or
+// -1.  Every wave computes it on its own (ballots over 64 sequences at a time),
+// so the lookup needs no workgroup barrier and the result is wave-uniform.
+__device__ __forceinline__ int find_seq(const int* s_ntq, int S, int t, int rank) {
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int src = lane >= d ? lane - d : lane;
-    const int t = __builtin_amdgcn_ds_bpermute(src << 2, v);
-    if (lane >= d) v += t;
+  for (int c0 = 0; c0 < S; c0 += 64) {
+    const int sq = c0 + lane;
+    const bool f = sq < S && s_ntq[sq] > t;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(f);
+    const int cnt = __builtin_popcountll(m);
+    if (rank < cnt) {
+      const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(f && below == rank);
+      return c0 + static_cast<int>(__builtin_ctzll(hit));
+    }
+    rank -= cnt;
   }
-  if (lane == 63) s_wsum[wv] = v;
-  __syncthreads();
-  int before = 0;
-  total = 0;
-#pragma unroll
-  for (int i = 0; i < kWaves; ++i) {
-    const int x = s_wsum[i];
-    before += i < wv ? x : 0;
-    total += x;
-  }
-  __syncthreads();
-  return v + before;
+  return -1;
 }
 
 template <bool PAGED, int D>
@@ -518,8 +609,6 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(
   __shared__ __attribute__((aligned(1024))) char smem_all[kStages * Geom<D>::kStageBytes];
   __shared__ int s_ntq[kPersistMaxSeqs];           // query tiles of each sequence
   __shared__ int s_start[kPersistMaxTiles + 1];    // first item of each tile level (level T_max: total)
-  __shared__ int s_wsum[kWaves];
-  __shared__ int s_found;
   const int tid = threadIdx.x;
   const int S = p.num_seqs;
   const int T = p.num_q_tiles;
@@ -577,43 +666,50 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(
   const int total = s_start[T];
   const int NW = static_cast<int>(gridDim.x);
   const int g = static_cast<int>(blockIdx.x);
-  for (int round = 0;; ++round) {
-    int q = g;
-    if (round & 1) q = (NW % 8 == 0) ? 8 * (NW / 8 - 1 - g / 8) + g % 8 : NW - 1 - g;
-    const int64_t item64 = static_cast<int64_t>(round) * NW + q;
-    if (item64 >= total) break;
-    const int item = static_cast<int>(item64);
-    // level t: the smallest t with start[t] <= item (start decreases in t)
-    int lo = 0, hi = T - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (s_start[mid] <= item) hi = mid;
-      else lo = mid + 1;
-    }
-    const int t = lo;
-    const int j = item - s_start[t];
-    int rank = j / nkv;
-    const int kvh = j - rank * nkv;
-    // the rank-th sequence (ascending) with more than t query tiles
-    int seq = -1;
-    for (int c0 = 0; c0 < S; c0 += kThreads) {
-      const int sq = c0 + tid;
-      const int f = sq < S && s_ntq[sq] > t ? 1 : 0;
-      int chunk;
-      const int incl = wg_scan_incl(f, s_wsum, chunk);
-      if (f && incl - 1 == rank) s_found = sq;
-      __syncthreads();
-      if (rank < chunk) {
-        seq = s_found;
-        break;
+  // This workgroup's next valid item from round `round` on (rounds advance
+  // past it); an invalid descriptor when none is left.
+  int round = 0;
+  auto next_item = [&]() {
+    for (;; ++round) {
+      int q = g;
+      if (round & 1) q = (NW % 8 == 0) ? 8 * (NW / 8 - 1 - g / 8) + g % 8 : NW - 1 - g;
+      const int64_t item64 = static_cast<int64_t>(round) * NW + q;
+      if (item64 >= total) return item_desc(p, -1, 0, 0);
+      const int item = static_cast<int>(item64);
+      // level t: the smallest t with start[t] <= item (start decreases in t)
+      int lo = 0, hi = T - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (__builtin_amdgcn_readfirstlane(s_start[mid]) <= item) hi = mid;
+        else lo = mid + 1;
       }
-      rank -= chunk;
+      const int t = lo;
+      const int j = item - __builtin_amdgcn_readfirstlane(s_start[t]);
+      const int rank = j / nkv;
+      const int kvh = j - rank * nkv;
+      const ItemDesc d = item_desc(p, find_seq(s_ntq, S, t, rank), kvh, t);
+      if (d.valid) {
+        ++round;
+        return d;
+      }
     }
-    if (seq < 0) continue;  // not reached with consistent cu_seqlens (uniform over the workgroup)
-    prefill_item<PAGED, D>(p, smem_all, seq, kvh, t);
-    __syncthreads();  // the ring is reused by the next item
+  };
+  ItemDesc cur = next_item();
+  if (!cur.valid) return;
+  bf16x8 qop[D / 16];
+  item_fetch_q<D>(p, cur, qop);
+  item_fetch_tiles<PAGED, D>(p, smem_all, cur);
+  for (;;) {
+    // the next item is located (and its cu_seqlens read) while this one's
+    // first copies are in flight; its own first copies start in this one's
+    // epilogue
+    const ItemDesc nxt = next_item();
+    prefill_run<PAGED, D>(p, smem_all, cur, qop, nxt);
+    if (!nxt.valid) break;
+    cur = nxt;
   }
 }
+
 
 int prefill_positions_per_tile(int group) { return group >= 1 && group <= kRows ? kRows / group : 1; }
 
