@@ -171,17 +171,17 @@ __device__ __forceinline__ void wait_vmem() {
 // swizzled (row, col) of StageLane.  Keys at or beyond kmax (only in the last
 // tile) are redirected to the tile's first key, a valid row whose scores the
 // masks remove.
-template <int P>
+template <int P, int U0 = 0, int U1 = P>
 __device__ __forceinline__ void dma_tile(char* st, const char* tile, const StageLane<P>& d, int kb, int kmax, int w,
                                          int v_skip) {
   const uint32_t dst = lds_addr(st) + v_skip + P * w * 1024;
   if (kb + kBK <= kmax) {
 #pragma unroll
-    for (int u = 0; u < P; ++u) dma16(tile, d.off[u], dst + u * 1024);
+    for (int u = U0; u < U1; ++u) dma16(tile, d.off[u], dst + u * 1024);
   } else {
     const int nrow = kmax - kb;
 #pragma unroll
-    for (int u = 0; u < P; ++u)
+    for (int u = U0; u < U1; ++u)
       dma16(tile, d.row[u] < nrow ? d.off[u] : static_cast<uint32_t>(d.col[u] * 2), dst + u * 1024);
   }
 }
@@ -276,6 +276,11 @@ struct ItemStaging {
   }
   __device__ __forceinline__ void copy(const PrefillParams& p, const ItemDesc& it, char* st, int page, int t) const {
     dma_tile<Geom<D>::P>(st, tile(p, it, page, t), dl, t * kBK, it.kmax, w, v_skip);
+  }
+  // pieces [U0, U1) of this wave's share of tile t, whose first key is at src
+  template <int U0, int U1>
+  __device__ __forceinline__ void copy_part(const ItemDesc& it, char* st, const char* src, int t) const {
+    dma_tile<Geom<D>::P, U0, U1>(st, src, dl, t * kBK, it.kmax, w, v_skip);
   }
 };
 
@@ -473,9 +478,13 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
     else
       wait_vmem<0>();
     barrier_lds();
-    if (it + 3 < ntiles) stg.copy(p, item, fill, page_ahead, it + 3);
-    if (PAGED && it + 4 < ntiles) page_ahead = page_of(p, stg.bt, kb + 4 * kBK);
+    // tile it+3's copy in two halves, one on each side of the second step, so
+    // its LDS writes do not all land at once among the operand reads
+    const char* src3 = stg.tile(p, item, page_ahead, it + 3);
+    if (it + 3 < ntiles) stg.template copy_part<0, P / 2>(item, fill, src3, it + 3);
     step(s1, s0, kb + 32, cur + 32 * RB, nxt, it + 1 < ntiles);
+    if (it + 3 < ntiles) stg.template copy_part<P / 2, P>(item, fill, src3, it + 3);
+    if (PAGED && it + 4 < ntiles) page_ahead = page_of(p, stg.bt, kb + 4 * kBK);
   };
 
   // prologue: tiles 0 and 1 (copies issued before this call) and the Q
