@@ -399,6 +399,16 @@ __device__ __forceinline__ int block_scan_incl(int v, int* s_wsum, int& total) {
 
 __device__ __forceinline__ int64_t range_start(int64_t r, int64_t T, int64_t P) { return r * T / P; }
 
+// Ranges used for T steps: the planned P, but no more than one per
+// kMinRangeSteps steps.  The host plans P from the block-table width, an upper
+// bound on the steps; short actual totals (small batches) would otherwise be
+// cut into one-step pieces whose partials the merge then has to fold.
+constexpr int64_t kMinRangeSteps = 4;
+__device__ __forceinline__ int64_t used_ranges(int64_t P, int64_t T) {
+  const int64_t cap = T / kMinRangeSteps;
+  return cap < 1 ? 1 : (P < cap ? P : cap);
+}
+
 template <bool FP8, int WAVES, bool PREFETCH, int D>
 __global__ __launch_bounds__(64 * WAVES) void paged_decode_balanced_kernel(DecodeParams p) {
   constexpr int CH = 64 * WAVES;  // sequences per scan chunk
@@ -421,7 +431,8 @@ __global__ __launch_bounds__(64 * WAVES) void paged_decode_balanced_kernel(Decod
     T += tot;
   }
   if (write_prefix && tid == 0) p.ws_prefix[B] = T;
-  const int64_t P = p.balanced_ranges;
+  const int64_t P = used_ranges(p.balanced_ranges, T);
+  if (r >= P) return;
   const int start = static_cast<int>(range_start(r, T, P));
   const int end = static_cast<int>(range_start(r + 1, T, P));
   if (start >= end) return;  // uniform over the workgroup
@@ -479,7 +490,7 @@ __global__ __launch_bounds__(64 * kMergeHeads) void decode_merge_kernel(DecodePa
   bool zero = false;
   if (p.balanced_ranges > 0) {
     const int64_t s0 = p.ws_prefix[b], s1 = p.ws_prefix[b + 1], T = p.ws_prefix[p.batch];
-    const int64_t P = p.balanced_ranges;
+    const int64_t P = used_ranges(p.balanced_ranges, T);
     if (s1 <= s0) {
       zero = true;
       first = count = 0;
@@ -499,10 +510,11 @@ __global__ __launch_bounds__(64 * kMergeHeads) void decode_merge_kernel(DecodePa
   if (h >= p.num_heads) return;
   // A partial slot holds data unless it is a balanced range with no steps (P > T).
   const int64_t T = p.balanced_ranges > 0 ? p.ws_prefix[p.batch] : 0;
+  const int64_t PU = p.balanced_ranges > 0 ? used_ranges(p.balanced_ranges, T) : 0;
   auto has_data = [&](int64_t s) {
     if (p.balanced_ranges <= 0) return true;
     const int64_t rr = first - b + s;
-    return range_start(rr, T, p.balanced_ranges) != range_start(rr + 1, T, p.balanced_ranges);
+    return range_start(rr, T, PU) != range_start(rr + 1, T, PU);
   };
   const bool cols = 2 * lane < p.head_dim;  // lane owns output columns 2 lane, 2 lane + 1
   float M = kNegInf, L = 0.f, o0 = 0.f, o1 = 0.f;

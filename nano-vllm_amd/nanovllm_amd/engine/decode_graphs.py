@@ -58,14 +58,15 @@ class DecodeGraphs:
         self.slot_mapping = torch.full((mb,), pad_slot, dtype=torch.int32, device=dev)
         self.context_lens = torch.zeros(mb, dtype=torch.int32, device=dev)
         self.block_tables = torch.zeros(mb, max_num_blocks, dtype=torch.int32, device=dev)
-        self.outputs = torch.zeros(len(layers), mb, nh * d, dtype=torch.bfloat16, device=dev)
+        # per graph size: the layers' outputs as the captured step produced them
+        # (graph-pool memory, rewritten by every replay of that graph)
+        self.layer_outputs: dict[int, list[torch.Tensor]] = {}
         self.graph_bs = graph_batch_sizes(self.max_bs)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.pool = None
 
-    def _step(self, bs: int) -> None:
-        for i, layer in enumerate(self.layers):
-            self.outputs[i, :bs] = layer(self.q[:bs], self.k[:bs], self.v[:bs])
+    def _step(self, bs: int) -> list[torch.Tensor]:
+        return [layer(self.q[:bs], self.k[:bs], self.v[:bs]) for layer in self.layers]
 
     @torch.inference_mode()
     def capture(self) -> "DecodeGraphs":
@@ -76,7 +77,7 @@ class DecodeGraphs:
                         block_tables=self.block_tables[:bs])
             self._step(bs)  # warmup
             with torch.cuda.graph(g, self.pool):
-                self._step(bs)
+                self.layer_outputs[bs] = self._step(bs)
             if self.pool is None:
                 self.pool = g.pool()
             self.graphs[bs] = g
@@ -86,15 +87,18 @@ class DecodeGraphs:
 
     @torch.inference_mode()
     def run(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
-            context_lens: torch.Tensor, block_tables: torch.Tensor) -> torch.Tensor:
-        """One decode step of every layer for bs = q.shape[0] rows; returns (L, bs, nh*d).
-        Sizes above the largest graph run eagerly (model_runner.py:264-265)."""
+            context_lens: torch.Tensor, block_tables: torch.Tensor) -> list[torch.Tensor]:
+        """One decode step of every layer for bs = q.shape[0] rows; returns the L layers'
+        (bs, nh*d) outputs.  From a graph these are views of the graph's own output tensors,
+        valid until its next replay (as run_model returns graph_vars["outputs"][:bs],
+        model_runner.py:281).  Sizes above the largest graph run eagerly
+        (model_runner.py:264-265)."""
         bs = q.shape[0]
         size = pick_graph_size(self.graph_bs, bs)
         if size is None or block_tables.shape[1] > self.max_num_blocks:
             set_context(False, slot_mapping=slot_mapping, context_lens=context_lens, block_tables=block_tables)
             try:
-                return torch.stack([layer(q, k, v) for layer in self.layers])
+                return [layer(q, k, v) for layer in self.layers]
             finally:
                 reset_context()
         # static buffers: zero, live rows in (model_runner.py:271-280); the slot pad is -1
@@ -111,4 +115,4 @@ class DecodeGraphs:
         self.context_lens[:bs] = context_lens
         self.block_tables[:bs, : block_tables.shape[1]] = block_tables
         self.graphs[size].replay()
-        return self.outputs[:, :bs]
+        return [o[:bs] for o in self.layer_outputs[size]]

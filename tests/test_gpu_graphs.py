@@ -83,7 +83,7 @@ def test_replay_matches_eager_and_skips_padding(dev):
     assert sorted(graphs.graphs) == [1, 2, 4, 8, 16, 32, 48]
     for i, bs in enumerate([1, 3, 16, 17, 40, 48]):
         batch = _batch(dev, bs, max_blocks - 1, num_blocks, seed=100 + i)
-        got = graphs.run(*batch)
+        got = torch.stack(graphs.run(*batch))
         ref = _eager(twins, *batch)
         torch.cuda.synchronize()
         assert got.shape == (2, bs, NH * D)
@@ -101,7 +101,7 @@ def test_batches_beyond_the_graphs_run_eagerly(dev):
     twins = _layers(dev, 1, 40, seed=5)
     graphs = DecodeGraphs(layers, max_bs=8, max_num_blocks=2).capture()
     batch = _batch(dev, 12, 2, 40, seed=9)
-    got = graphs.run(*batch)
+    got = torch.stack(graphs.run(*batch))
     ref = _eager(twins, *batch)
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
