@@ -469,7 +469,39 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
   // Paged caches: block id of the next tile to copy, read one tile ahead so
   // the scalar load's latency is covered by a tile of math (its wait falls in
   // the next barrier, which waits for lgkmcnt anyway).
-  int page_ahead = PAGED && 3 < ntiles ? page_of(p, stg.bt, 3 * kBK) : 0;
+  // Cursor over the tiles still to copy (from tile 2 on): c_ptr is the first
+  // key of the next one.  Inside a page it moves by one tile of rows; at a
+  // page boundary it takes the page id read one page earlier (a block id
+  // outside the pool redirects to slot 0).  Block sizes are multiples of 64,
+  // so a tile never straddles two pages.  This replaces a division and a
+  // 64-bit multiply per tile.
+  const int64_t tile_step = static_cast<int64_t>(kBK) * stg.dstride * 2;
+  const int tpp = PAGED ? p.block_size / kBK : 1;  // tiles per page
+  const uint32_t nb32 = p.num_blocks > 0x7fffffff ? 0x7fffffffu : static_cast<uint32_t>(p.num_blocks);
+  auto page_at = [&](int idx) { return idx < p.max_blocks ? stg.bt[idx] : -1; };
+  auto page_base = [&](int page) {
+    const int64_t slot = static_cast<uint32_t>(page) < nb32 ? static_cast<int64_t>(page) * p.block_size : 0;
+    return reinterpret_cast<const char*>(stg.dbase + slot * stg.dstride);
+  };
+  int c_pg = PAGED ? 2 / tpp : 0;        // block-table index of the next tile's page
+  int c_left = PAGED ? tpp - 2 % tpp : 0;  // tiles of that page from the next one on
+  int c_next = PAGED ? page_at(c_pg + 1) : 0;
+  const char* c_ptr = PAGED ? page_base(page_at(c_pg)) + (2 % tpp) * tile_step
+                            : reinterpret_cast<const char*>(stg.dbase + (static_cast<int64_t>(item.k_start) + 2 * kBK) * stg.dstride);
+  auto advance = [&]() {
+    if constexpr (PAGED) {
+      if (--c_left > 0) {
+        c_ptr += tile_step;
+      } else {
+        ++c_pg;
+        c_left = tpp;
+        c_ptr = page_base(c_next);
+        c_next = page_at(c_pg + 1);  // scalar load, a page of tiles ahead of its use
+      }
+    } else {
+      c_ptr += tile_step;
+    }
+  };
   auto tile_iter = [&](int it, const char* cur, const char* nxt, char* fill) {
     const int kb = it * kBK;
     step(s0, s1, kb, cur, cur + 32 * RB, true);
@@ -480,11 +512,13 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
     barrier_lds();
     // tile it+3's copy in two halves, one on each side of the second step, so
     // its LDS writes do not all land at once among the operand reads
-    const char* src3 = stg.tile(p, item, page_ahead, it + 3);
-    if (it + 3 < ntiles) stg.template copy_part<0, P / 2>(item, fill, src3, it + 3);
+    const char* src3 = c_ptr;
+    if (it + 3 < ntiles) {
+      stg.template copy_part<0, P / 2>(item, fill, src3, it + 3);
+      advance();
+    }
     step(s1, s0, kb + 32, cur + 32 * RB, nxt, it + 1 < ntiles);
     if (it + 3 < ntiles) stg.template copy_part<P / 2, P>(item, fill, src3, it + 3);
-    if (PAGED && it + 4 < ntiles) page_ahead = page_of(p, stg.bt, kb + 4 * kBK);
   };
 
   // prologue: tiles 0 and 1 (copies issued before this call) and the Q
@@ -499,7 +533,10 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks) asm volatile("" ::"v"(qop[ks]));
   barrier_lds();
-  if (2 < ntiles) stg.copy(p, item, stage(2), PAGED ? page_of(p, stg.bt, 2 * kBK) : 0, 2);
+  if (2 < ntiles) {
+    stg.template copy_part<0, P>(item, stage(2), c_ptr, 2);
+    advance();
+  }
   if (0 < wave_kmax) qk(stage(0), s0);
   // Use the softmax scale (a kernel-argument scalar load) once here, so its
   // wait lands in the prologue rather than on the first use inside the loop,
