@@ -400,11 +400,11 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
       bf16x8 kr[NKS];
       k_read(next ? sb_next : sb_v, kr);
       if (key0 + 32 > wave_full || key0 + 32 > kmax) {
+        // score i is key key0 + 4h + c_i (c_i = 8 (i / 4) + i % 4): it stays
+        // when c_i <= limit - key0 - 4h, one compare against an immediate each
+        const int rel = limit - key0 - 4 * h;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = key0 + 8 * (i >> 2) + 4 * h + (i & 3);
-          sv[i] = key <= limit ? sv[i] : kNegInf;
-        }
+        for (int i = 0; i < 16; ++i) sv[i] = 8 * (i >> 2) + (i & 3) <= rel ? sv[i] : kNegInf;
       }
       float mx = sv[0];
 #pragma unroll
