@@ -76,8 +76,8 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 // Workgroup barrier after this wave's LDS accesses have completed.  Unlike
-// __syncthreads it does not also wait for the global loads still in flight
-// (the tile staged in registers one tile ahead).
+// __syncthreads it does not also wait for the tile copies still in flight;
+// those are waited for explicitly (wait_vmem) where a tile must be complete.
 __device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ bf16x8 read_tr_pair(const char* p0, const char* p1) {
@@ -466,15 +466,12 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
   // Scores ping-pong between two buffers: the first step of a tile reads s0
   // and issues the QK of the second into s1, which issues the next tile's into s0.
   f32x16 s0 = f32x16{}, s1 = f32x16{};
-  // Paged caches: block id of the next tile to copy, read one tile ahead so
-  // the scalar load's latency is covered by a tile of math (its wait falls in
-  // the next barrier, which waits for lgkmcnt anyway).
   // Cursor over the tiles still to copy (from tile 2 on): c_ptr is the first
   // key of the next one.  Inside a page it moves by one tile of rows; at a
   // page boundary it takes the page id read one page earlier (a block id
   // outside the pool redirects to slot 0).  Block sizes are multiples of 64,
-  // so a tile never straddles two pages.  This replaces a division and a
-  // 64-bit multiply per tile.
+  // so a tile never straddles two pages, and the loop needs no division and
+  // no 64-bit multiply per tile.
   const int64_t tile_step = static_cast<int64_t>(kBK) * stg.dstride * 2;
   const int tpp = PAGED ? p.block_size / kBK : 1;  // tiles per page
   const uint32_t nb32 = p.num_blocks > 0x7fffffff ? 0x7fffffffu : static_cast<uint32_t>(p.num_blocks);
