@@ -143,6 +143,50 @@ def bench_prefill(case, steps, warmup, warm_s=1.0):
     return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
 
 
+def bench_store(case, steps, warmup, warm_s=1.0, n_pools=8):
+    """store_kvcache of a prefill case's fresh tokens (the bandwidth case of the
+    scatter).  Calls rotate over n_pools copies of the sources (k, and v as the
+    same strided view of a wider buffer) and of the destination caches, so the
+    rotation's footprint exceeds the 256 MB Infinity Cache.  Per-call time is
+    the replay time of a graph of n_pools calls divided by n_pools."""
+    import torch
+    import nanovllm_amd as nva
+    pools = []
+    for _ in range(n_pools):
+        k = case.k.clone()
+        v = torch.empty_strided(case.v.shape, case.v.stride(), dtype=case.v.dtype, device=case.v.device)
+        v.copy_(case.v)
+        pools.append((k, v, torch.empty_like(case.k_cache), torch.empty_like(case.v_cache)))
+
+    def run(i):
+        k, v, kc, vc = pools[i % n_pools]
+        nva.store_kvcache(k, v, kc, vc, case.slot_mapping)
+
+    # One call per pool captured in a HIP graph and replayed: a store of this
+    # size takes less time on the GPU than the Python wrapper takes to issue
+    # it, so timing eager calls would time the host.
+    _warm(run, warmup, warm_s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_pools):
+            run(i)
+    reps = max(4, steps // n_pools)
+    for _ in range(3):
+        g.replay()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (reps * n_pools)
+    del g
+    nbytes = case.store_bytes()
+    del pools
+    return dict(ms=ms, tokens=sum(case.lens_q), bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9,
+                frac=nbytes / (ms * 1e-3) / 8.0e12)
+
+
 def bench_producer(case, steps, warmup, warm_s=1.0):
     """The fused qk-RMSNorm + rotary step (nva_qk_norm_rope) over config 4's tokens."""
     import torch
@@ -290,11 +334,17 @@ def main(argv=None):
         c4 = W.config4(dev)
         out["cfg4"] = bench_prefill(c4, max(10, steps // 2), warmup, args.warm_seconds)
         log(f"[bench] cfg4 {out['cfg4']['ms']*1e3:.1f} us = {out['cfg4']['tflops']:.0f} TFLOP/s")
+        out["store4"] = bench_store(c4, steps, warmup, args.warm_seconds)
+        log(f"[bench] cfg4 store_kvcache {out['store4']['tokens']} tokens {out['store4']['ms']*1e3:.1f} us "
+            f"= {out['store4']['gbs']:.0f} GB/s ({out['store4']['frac']:.3f} of 8 TB/s)")
         del c4
         log("[bench] config 2: varlen prefill")
         c2 = W.config2(dev)
         out["cfg2"] = bench_prefill(c2, max(10, steps // 2), warmup, args.warm_seconds)
         log(f"[bench] cfg2 {out['cfg2']['ms']*1e3:.1f} us = {out['cfg2']['tflops']:.0f} TFLOP/s")
+        out["store2"] = bench_store(c2, steps, warmup, args.warm_seconds)
+        log(f"[bench] cfg2 store_kvcache {out['store2']['tokens']} tokens {out['store2']['ms']*1e3:.1f} us "
+            f"= {out['store2']['gbs']:.0f} GB/s ({out['store2']['frac']:.3f} of 8 TB/s)")
         del c2
         torch.cuda.empty_cache()
     if args.only in (None, "producer"):
@@ -343,6 +393,11 @@ def main(argv=None):
                                "gflop": round(out[k]["flops"] / 1e9, 2),
                                "frac_bf16_peak": round(out[k]["tflops"] / BF16_PEAK_TFLOPS, 4)}
                            for k in ("cfg4", "cfg2") if k in out}
+    if "store4" in out or "store2" in out:
+        line["store_kvcache_prefill"] = {
+            k: {"tokens": out[s]["tokens"], "us": round(out[s]["ms"] * 1e3, 2), "bytes": out[s]["bytes"],
+                "gbs": round(out[s]["gbs"], 1), "frac": round(out[s]["frac"], 4)}
+            for k, s in (("cfg4", "store4"), ("cfg2", "store2")) if s in out}
     if "cfg5" in out:
         d5 = out["cfg5"]
         line["fp8_decode"] = {"cfg5": {"gbs": round(d5["attn_gbs"], 1), "frac": round(d5["attn_gbs"] / HBM_PEAK_GBS, 4),
