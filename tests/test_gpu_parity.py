@@ -541,6 +541,40 @@ def test_prefill_persistent_many_sequences(dev, nh, nkv, d, prefix):
     assert_attn_close(got, prefill_reference(case), what=f"persistent prefill nh={nh} nkv={nkv} d={d} prefix={prefix}")
 
 
+@pytest.mark.parametrize("block_size,prefix_pages", [(64, 3), (128, 2), (512, 1), (768, 1)])
+def test_prefill_paged_block_sizes(dev, block_size, prefix_pages):
+    """Prefix-cached prefill over caches paged at block sizes other than 256: the
+    kernel walks a sequence's tiles page by page (one tile per page at 64, a
+    first tile in the middle of a page at 768), direct grid."""
+    from nanovllm_amd import workloads as W
+    lens = [1, 100, 333, 64, 0, 700]
+    prefix = prefix_pages * block_size
+    pages = sum(-(-(prefix + x) // block_size) for x in lens) + 4
+    case = W.make_prefill_case(lens, 16, 8, pages, prefix_len=prefix, block_size=block_size,
+                               seed=block_size + prefix_pages, bulk_device=dev, shared_prefix=False)
+    got = _run_prefill(case)
+    assert_attn_close(got, prefill_reference(case), what=f"block_size={block_size} prefix={prefix}")
+
+
+@pytest.mark.parametrize("block_size", [64, 512])
+def test_prefill_persistent_block_sizes(dev, block_size):
+    """The persistent grid (more than twice the CU count of items) over caches
+    paged at 64 and 512 keys, with a shared cached prefix."""
+    from nanovllm_amd import workloads as W
+    gen = torch.Generator().manual_seed(950 + block_size)
+    S = 24
+    lens = torch.randint(0, 401, (S,), generator=gen).tolist()
+    lens[5] = 0
+    lens[S - 1] = 900
+    prefix = 512
+    pages = sum(-(-(prefix + x) // block_size) for x in lens) + 4
+    case = W.make_prefill_case(lens, 32, 8, pages, prefix_len=prefix, block_size=block_size,
+                               seed=951 + block_size, bulk_device=dev, shared_prefix=True)
+    assert S * 8 * -(-max(lens) // 64) > 2 * 256  # the persistent grid serves this call
+    got = _run_prefill(case)
+    assert_attn_close(got, prefill_reference(case), what=f"persistent block_size={block_size}")
+
+
 @pytest.mark.parametrize("prefix", [0, 256])
 def test_prefill_head_dim_64(dev, prefix):
     from nanovllm_amd import workloads as W
