@@ -541,6 +541,26 @@ def test_prefill_persistent_many_sequences(dev, nh, nkv, d, prefix):
     assert_attn_close(got, prefill_reference(case), what=f"persistent prefill nh={nh} nkv={nkv} d={d} prefix={prefix}")
 
 
+@pytest.mark.parametrize("prefix", [0, 256])
+def test_prefill_more_sequences_than_the_persistent_tables(dev, prefix):
+    """Over 1024 sequences the persistent grid's tables do not fit its LDS and
+    the direct grid serves the call: 1100 short ragged sequences, some empty."""
+    from nanovllm_amd import workloads as W
+    gen = torch.Generator().manual_seed(1100 + prefix)
+    S = 1100
+    lens = torch.randint(0, 41, (S,), generator=gen).tolist()
+    for i in range(0, S, 97):
+        lens[i] = 0
+    lens[S - 1] = 300
+    pages = (S if prefix else 0) + sum(-(-x // 256) for x in lens) + 4
+    case = W.make_prefill_case(lens, 16, 8, pages, prefix_len=prefix, seed=1101 + prefix, bulk_device=dev,
+                               shared_prefix=False)
+    got = _run_prefill(case)
+    seqs = list(range(0, S, 53)) + [S - 1]
+    ref = prefill_reference(case, seqs)
+    assert_attn_close(got[rows_of(case, seqs)], ref, what=f"{S} sequences prefix={prefix}")
+
+
 @pytest.mark.parametrize("block_size,prefix_pages", [(64, 3), (128, 2), (512, 1), (768, 1)])
 def test_prefill_paged_block_sizes(dev, block_size, prefix_pages):
     """Prefix-cached prefill over caches paged at block sizes other than 256: the
