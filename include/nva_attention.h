@@ -87,6 +87,12 @@ int nva_store_kvcache(const void* key, int64_t key_row_stride,
  * keys sees keys j <= i + (Lk - Lq).  A query row with no visible key yields zeros.
  * max_seqlen_q bounds the launch grid (host value, graph-capture safe).
  * head_dim 64 or 128; a paged cache needs block_size % 64 == 0 and bf16.
+ * workspace: NULL, or nva_prefill_workspace_bytes() bytes, 256-byte aligned, holding
+ *   zeros before its first use.  With it, a prefill over many work items hands them out
+ *   dynamically (a work queue per XCD); every completed call leaves the workspace zero
+ *   again, so it is allocated and cleared once and reused.  Calls that may run at the
+ *   same time (different streams) need different workspaces.  NULL selects a static
+ *   item order; the results are bit-identical either way.
  */
 int nva_prefill(const void* q, int64_t q_row_stride,
                 const void* k, int64_t k_row_stride,
@@ -97,7 +103,11 @@ int nva_prefill(const void* q, int64_t q_row_stride,
                 int32_t num_seqs, int32_t max_seqlen_q, int32_t max_seqlen_k,
                 int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                 float softmax_scale,
-                void* out, int64_t out_row_stride, void* stream);
+                void* out, int64_t out_row_stride,
+                void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Bytes of the optional nva_prefill workspace (a constant of the library). */
+int64_t nva_prefill_workspace_bytes(void);
 
 /*
  * Workspace bytes nva_decode needs for these launch parameters (0 if it needs none).

@@ -111,7 +111,8 @@ int nva_prefill(const void* q, int64_t q_row_stride, const void* k, int64_t k_ro
                 int32_t max_blocks_per_seq, int32_t block_size, int64_t num_blocks,
                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
                 int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads, int32_t num_kv_heads,
-                int32_t head_dim, float softmax_scale, void* out, int64_t out_row_stride, void* stream) {
+                int32_t head_dim, float softmax_scale, void* out, int64_t out_row_stride, void* workspace,
+                int64_t workspace_bytes, void* stream) {
   (void)max_seqlen_k;
   if (head_dim != 128 && head_dim != 64)
     return fail(NVA_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", head_dim);
@@ -151,6 +152,9 @@ int nva_prefill(const void* q, int64_t q_row_stride, const void* k, int64_t k_ro
       return fail(NVA_ERR_INVALID_ARGUMENT, "block table shape is inconsistent");
     if (!aligned(block_table, 4)) return fail(NVA_ERR_INVALID_ARGUMENT, "block_table must be 4-byte aligned");
   }
+  if (workspace && (workspace_bytes < nva::kPrefillWorkspaceBytes || !aligned(workspace, 256)))
+    return fail(NVA_ERR_INVALID_ARGUMENT, "prefill workspace must be 256-byte aligned and hold %lld bytes",
+                static_cast<long long>(nva::kPrefillWorkspaceBytes));
   nva::PrefillParams p{};
   p.q = static_cast<const uint16_t*>(q);
   p.k = static_cast<const uint16_t*>(k);
@@ -173,8 +177,11 @@ int nva_prefill(const void* q, int64_t q_row_stride, const void* k, int64_t k_ro
   p.group = num_heads / num_kv_heads;
   p.head_dim = head_dim;
   p.scale_log2 = softmax_scale * kLog2e;
+  p.queue = static_cast<uint32_t*>(workspace);
   return hip_status(nva::launch_prefill(p, max_seqlen_q, static_cast<hipStream_t>(stream)), "prefill launch");
 }
+
+int64_t nva_prefill_workspace_bytes(void) { return nva::kPrefillWorkspaceBytes; }
 
 int64_t nva_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                    int32_t max_blocks_per_seq, int32_t block_size, int32_t kv_dtype,

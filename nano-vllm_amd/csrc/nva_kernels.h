@@ -77,6 +77,7 @@ struct PrefillParams {
   int32_t positions_per_tile; // query positions per workgroup (x group = rows)
   int32_t head_dim;           // 64 or 128
   float scale_log2;
+  uint32_t* queue;            // null: static item order; else kPrefillQueueWords zeroed words
 };
 
 struct QKNormRopeParams {
@@ -101,6 +102,12 @@ hipError_t launch_decode(const DecodeParams& p, int kv_dtype, hipStream_t stream
 hipError_t launch_prefill(const PrefillParams& p, int max_seqlen_q, hipStream_t stream);
 int prefill_positions_per_tile(int group);  // query positions one prefill workgroup covers
 constexpr int kPrefillMaxGroup = 256;        // rows per prefill workgroup bound the GQA group
+// Work queue of the persistent prefill grid: one claim counter per XCD lane,
+// then the count of finished workgroups.  Zero on entry, zero again on exit.
+constexpr int kPrefillQueueLanes = 8;
+constexpr int kPrefillQueueWords = kPrefillQueueLanes + 1;
+constexpr int64_t kPrefillWorkspaceBytes = 256;
+static_assert(kPrefillQueueWords * 4 <= kPrefillWorkspaceBytes, "queue fits the workspace");
 
 // Split-K plan shared by nva_decode and nva_decode_workspace_bytes.
 // balanced_ranges > 0: balanced mode with that many step ranges; otherwise

@@ -301,7 +301,8 @@ __device__ __forceinline__ void item_fetch_tiles(const PrefillParams& p, char* s
 // epilogue's transpose therefore uses ring stages 2 and 3 only.
 template <bool PAGED, int D>
 __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_all, const ItemDesc& item,
-                                            bf16x8 (&qop)[D / 16], const ItemDesc& next) {
+                                            bf16x8 (&qop)[D / 16], const ItemDesc& next, uint32_t* claim_ctr,
+                                            uint32_t& claim) {
   using Gm = Geom<D>;
   constexpr int RB = Gm::RB;
   constexpr int KP = Gm::KP;
@@ -558,6 +559,9 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
   barrier_lds();  // every wave is done with the ring
   // stages 0 and 1 take the next item's first tiles
   if (next.valid) item_fetch_tiles<PAGED, D>(p, smem_all, next);
+  // A work-queue grid claims the item after `next` here, one item ahead; the
+  // caller reads the result after its own barrier, once the epilogue has run.
+  if (claim_ctr != nullptr && next.valid && threadIdx.x == 0) claim = atomicAdd(claim_ctr, 1u);
   // Each wave owns 32 rows in ring stages 2 and 3 (waves 0..3 in the K half,
   // 4..7 in the V half, two waves per tile): row n at n * RB, 16-byte chunk c
   // (dims 8c .. 8c+7) at position c ^ k_swz(n).  Read back, KP consecutive
@@ -606,7 +610,8 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   item_fetch_tiles<PAGED, D>(p, smem_all, it);
   ItemDesc none{};
   none.valid = false;
-  prefill_run<PAGED, D>(p, smem_all, it, qop, none);
+  uint32_t unused = 0;
+  prefill_run<PAGED, D>(p, smem_all, it, qop, none, nullptr, unused);
 }
 
 // Persistent grid: one workgroup per CU walks the real work items.
@@ -622,6 +627,15 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
 // their totals).  Workgroup g = 8 m + x runs on XCD x, and the snake reverses
 // m only, so one kv head's items stay on one XCD (and its L2) when
 // num_kv_heads is 8.
+//
+// With a work queue (p.queue) the order after the first item is dynamic
+// instead: lane x = g % 8 (the XCD) owns items 8 k + x, its workgroups start
+// with k = g / 8 and then claim k = NW / 8 + queue[x]++, each claim issued in
+// the previous item's epilogue so its latency is hidden.  A workgroup that
+// meets a slow CU or a heavy item simply claims fewer; a static order cannot
+// adapt (measured per-workgroup end times spread over ~75 us of ~225 us at
+// config 4).  The last workgroup to finish (queue[8] counts them) zeroes the
+// queue, so every completed launch leaves it as it found it.
 constexpr int kPersistMaxSeqs = 1024;
 constexpr int kPersistMaxTiles = 1024;
 constexpr int kThreads = 64 * kWaves;
@@ -647,11 +661,12 @@ __device__ __forceinline__ int find_seq(const int* s_ntq, int S, int t, int rank
   return -1;
 }
 
-template <bool PAGED, int D>
+template <bool PAGED, int D, bool QUEUE>
 __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(1024))) char smem_all[kStages * Geom<D>::kStageBytes];
   __shared__ int s_ntq[kPersistMaxSeqs];           // query tiles of each sequence
   __shared__ int s_start[kPersistMaxTiles + 1];    // first item of each tile level (level T_max: total)
+  __shared__ uint32_t s_claim;                     // the queue claim, broadcast by thread 0
   const int tid = threadIdx.x;
   const int S = p.num_seqs;
   const int T = p.num_q_tiles;
@@ -709,48 +724,62 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(
   const int total = s_start[T];
   const int NW = static_cast<int>(gridDim.x);
   const int g = static_cast<int>(blockIdx.x);
-  // This workgroup's next valid item from round `round` on (rounds advance
-  // past it); an invalid descriptor when none is left.
-  int round = 0;
-  auto next_item = [&]() {
-    for (;; ++round) {
-      int q = g;
-      if (round & 1) q = (NW % 8 == 0) ? 8 * (NW / 8 - 1 - g / 8) + g % 8 : NW - 1 - g;
-      const int64_t item64 = static_cast<int64_t>(round) * NW + q;
-      if (item64 >= total) return item_desc(p, -1, 0, 0);
-      const int item = static_cast<int>(item64);
-      // level t: the smallest t with start[t] <= item (start decreases in t)
-      int lo = 0, hi = T - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (__builtin_amdgcn_readfirstlane(s_start[mid]) <= item) hi = mid;
-        else lo = mid + 1;
-      }
-      const int t = lo;
-      const int j = item - __builtin_amdgcn_readfirstlane(s_start[t]);
-      const int rank = j / nkv;
-      const int kvh = j - rank * nkv;
-      const ItemDesc d = item_desc(p, find_seq(s_ntq, S, t, rank), kvh, t);
-      if (d.valid) {
-        ++round;
-        return d;
-      }
+  // Table item `item` (every item below `total` is a real tile: its sequence
+  // has more than t query tiles), or an invalid descriptor past the end.
+  auto desc_of = [&](int item) {
+    if (item >= total) return item_desc(p, -1, 0, 0);
+    // level t: the smallest t with start[t] <= item (start decreases in t)
+    int lo = 0, hi = T - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (__builtin_amdgcn_readfirstlane(s_start[mid]) <= item) hi = mid;
+      else lo = mid + 1;
+    }
+    const int t = lo;
+    const int j = item - __builtin_amdgcn_readfirstlane(s_start[t]);
+    const int rank = j / nkv;
+    const int kvh = j - rank * nkv;
+    return item_desc(p, find_seq(s_ntq, S, t, rank), kvh, t);
+  };
+  // QUEUE: the launch guarantees NW % 8 == 0, so lane x is the XCD
+  constexpr int L = kPrefillQueueLanes;
+  const int x = g % L;
+  uint32_t* const claim_ctr = QUEUE ? p.queue + x : nullptr;
+  auto finish = [&]() {
+    if (QUEUE && tid == 0 &&
+        atomicAdd(p.queue + kPrefillQueueLanes, 1u) == static_cast<uint32_t>(NW - 1)) {
+      for (int y = 0; y < kPrefillQueueWords; ++y) atomicExch(p.queue + y, 0u);
     }
   };
-  ItemDesc cur = next_item();
-  if (!cur.valid) return;
+  ItemDesc cur = desc_of(g);  // round 0 of either order
+  if (!cur.valid) {
+    finish();
+    return;
+  }
+  uint32_t claim = 0;
+  if (QUEUE && tid == 0) claim = atomicAdd(claim_ctr, 1u);
   bf16x8 qop[D / 16];
   item_fetch_q<D>(p, cur, qop);
   item_fetch_tiles<PAGED, D>(p, smem_all, cur);
-  for (;;) {
+  for (int round = 1;; ++round) {
     // the next item is located (and its cu_seqlens read) while this one's
     // first copies are in flight; its own first copies start in this one's
     // epilogue
-    const ItemDesc nxt = next_item();
-    prefill_run<PAGED, D>(p, smem_all, cur, qop, nxt);
+    ItemDesc nxt;
+    if (QUEUE) {
+      if (tid == 0) s_claim = claim;
+      __syncthreads();
+      nxt = desc_of(L * (NW / L + static_cast<int>(__builtin_amdgcn_readfirstlane(s_claim))) + x);
+    } else {
+      const int q = (round & 1) ? (NW % 8 == 0 ? 8 * (NW / 8 - 1 - g / 8) + g % 8 : NW - 1 - g) : g;
+      const int64_t item64 = static_cast<int64_t>(round) * NW + q;
+      nxt = desc_of(item64 < total ? static_cast<int>(item64) : total);
+    }
+    prefill_run<PAGED, D>(p, smem_all, cur, qop, nxt, claim_ctr, claim);
     if (!nxt.valid) break;
     cur = nxt;
   }
+  finish();
 }
 
 
@@ -780,20 +809,26 @@ hipError_t launch_prefill(const PrefillParams& p0, int max_seqlen_q, hipStream_t
   const int64_t max_items = static_cast<int64_t>(p.num_seqs) * p.num_kv_heads * p.num_q_tiles;
   const int cus = device_cu_count();
   if (p.num_seqs <= kPersistMaxSeqs && p.num_q_tiles <= kPersistMaxTiles && max_items > 2 * int64_t{cus}) {
-    // one workgroup per CU (the ring takes most of a CU's LDS)
+    // one workgroup per CU (the ring takes most of a CU's LDS); the work queue
+    // needs whole XCD lanes
     const unsigned nw = static_cast<unsigned>(cus);
     const dim3 grid(nw);
+    const bool queue = p.queue != nullptr && nw % kPrefillQueueLanes == 0;
+#define NVA_PERSIST(PG, DD)                                                                                  \
+  do {                                                                                                       \
+    if (queue)                                                                                               \
+      hipLaunchKernelGGL((varlen_prefill_persistent_kernel<PG, DD, true>), grid, dim3(kThreads), 0, stream, p); \
+    else                                                                                                     \
+      hipLaunchKernelGGL((varlen_prefill_persistent_kernel<PG, DD, false>), grid, dim3(kThreads), 0, stream, p); \
+  } while (0)
     if (p.head_dim == 64) {
-      if (p.block_table)
-        hipLaunchKernelGGL((varlen_prefill_persistent_kernel<true, 64>), grid, dim3(kThreads), 0, stream, p);
-      else
-        hipLaunchKernelGGL((varlen_prefill_persistent_kernel<false, 64>), grid, dim3(kThreads), 0, stream, p);
+      if (p.block_table) NVA_PERSIST(true, 64);
+      else NVA_PERSIST(false, 64);
     } else {
-      if (p.block_table)
-        hipLaunchKernelGGL((varlen_prefill_persistent_kernel<true, 128>), grid, dim3(kThreads), 0, stream, p);
-      else
-        hipLaunchKernelGGL((varlen_prefill_persistent_kernel<false, 128>), grid, dim3(kThreads), 0, stream, p);
+      if (p.block_table) NVA_PERSIST(true, 128);
+      else NVA_PERSIST(false, 128);
     }
+#undef NVA_PERSIST
     return hipGetLastError();
   }
   const dim3 grid(static_cast<unsigned>(p.num_seqs * p.num_kv_heads), static_cast<unsigned>(p.num_q_tiles));

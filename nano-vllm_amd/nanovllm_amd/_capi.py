@@ -43,8 +43,10 @@ SIGNATURES = {
         _c_void_p, _i64, _i32, _i32, _i64,  # block_table, bt_row_stride, max_blocks, block_size, num_blocks
         _c_void_p, _c_void_p, _i32, _i32, _i32,  # cu_q, cu_k, num_seqs, max_seqlen_q, max_seqlen_k
         _i32, _i32, _i32, _f32,            # num_heads, num_kv_heads, head_dim, softmax_scale
-        _c_void_p, _i64, _c_void_p,        # out, out_row_stride, stream
+        _c_void_p, _i64,                   # out, out_row_stride
+        _c_void_p, _i64, _c_void_p,        # workspace, workspace_bytes, stream
     ]),
+    "nva_prefill_workspace_bytes": (_i64, []),
     "nva_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "nva_decode": (_i32, [
         _c_void_p, _i64,                   # q, q_row_stride

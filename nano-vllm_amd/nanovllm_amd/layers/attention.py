@@ -41,6 +41,25 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+# One prefill work-queue workspace per (device, stream): zeroed once, and every
+# completed nva_prefill call leaves it zero again.  Calls on one stream run one
+# after another, so they can share it; different streams get their own.
+_PREFILL_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _prefill_workspace(device: torch.device, stream: int) -> torch.Tensor | None:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _PREFILL_WORKSPACES.get(key)
+    if ws is None:
+        # A zero fill recorded into a graph under capture would not run until the
+        # graph replays, so such a call takes the static item order instead.
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        ws = torch.zeros(int(_capi.load().nva_prefill_workspace_bytes()), dtype=torch.uint8, device=device)
+        _PREFILL_WORKSPACES[key] = ws
+    return ws
+
+
 def _cache_dtype_code(cache: torch.Tensor) -> int:
     if cache.dtype == _BF16:
         return _capi.NVA_DTYPE_BF16
@@ -129,11 +148,14 @@ def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ma
         k_row, v_row = k.stride(0), v.stride(0)
         bt_ptr, bt_stride, max_blocks, block_size, num_blocks = None, 0, 0, 0, 0
     lib = _capi.load()
+    stream = _stream(q)
+    ws = _prefill_workspace(q.device, stream)
     _capi.check(lib.nva_prefill(
         q.data_ptr(), q.stride(0), k.data_ptr(), k_row, v.data_ptr(), v_row,
         bt_ptr, bt_stride, max_blocks, block_size, num_blocks,
         cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), num_seqs, int(max_seqlen_q), int(max_seqlen_k),
-        nh, nkv, d, float(softmax_scale), out.data_ptr(), out.stride(0), _stream(q)))
+        nh, nkv, d, float(softmax_scale), out.data_ptr(), out.stride(0),
+        _ptr(ws), 0 if ws is None else ws.numel(), stream))
     return out
 
 

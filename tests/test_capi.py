@@ -33,7 +33,8 @@ def declared_functions():
 
 def test_header_lists_entry_points():
     names = declared_functions()
-    assert {"nva_store_kvcache", "nva_prefill", "nva_decode", "nva_decode_workspace_bytes",
+    assert {"nva_store_kvcache", "nva_prefill", "nva_prefill_workspace_bytes", "nva_decode",
+            "nva_decode_workspace_bytes",
             "nva_last_error", "nva_version", "nva_qk_norm_rope"} <= set(names)
 
 
@@ -82,7 +83,8 @@ def prefill(lib, **kw):
     args = dict(q=A, q_row_stride=2048, k=B, k_row_stride=1024, v=C, v_row_stride=4096, block_table=None,
                 bt_row_stride=0, max_blocks=0, block_size=0, num_blocks=0, cu_q=A + 0x9000, cu_k=A + 0xA000,
                 num_seqs=2, max_seqlen_q=100, max_seqlen_k=100, num_heads=16, num_kv_heads=8, head_dim=128,
-                scale=0.088, out=C + 0x200000, out_row_stride=2048, stream=None)
+                scale=0.088, out=C + 0x200000, out_row_stride=2048, workspace=None, workspace_bytes=0,
+                stream=None)
     args.update(kw)
     return lib.nva_prefill(*args.values())
 
@@ -99,6 +101,8 @@ def prefill(lib, **kw):
     (dict(scale=0.0), _capi.NVA_ERR_INVALID_ARGUMENT),
     (dict(block_table=A, bt_row_stride=8, max_blocks=8, block_size=32, num_blocks=10), _capi.NVA_ERR_UNSUPPORTED),
     (dict(block_table=A, bt_row_stride=4, max_blocks=8, block_size=256, num_blocks=10), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(workspace=A + 0x100000, workspace_bytes=128), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(workspace=A + 0x100040, workspace_bytes=256), _capi.NVA_ERR_INVALID_ARGUMENT),
 ])
 def test_prefill_rejects(lib, kw, code):
     assert prefill(lib, **kw) == code
@@ -107,6 +111,11 @@ def test_prefill_rejects(lib, kw, code):
 def test_prefill_empty_is_noop(lib):
     assert prefill(lib, num_seqs=0, q=None) == _capi.NVA_OK
     assert prefill(lib, max_seqlen_q=0) == _capi.NVA_OK
+
+
+def test_prefill_workspace_bytes(lib):
+    n = lib.nva_prefill_workspace_bytes()
+    assert n >= 4 * 9 and n % 256 == 0
 
 
 def decode(lib, **kw):

@@ -541,6 +541,36 @@ def test_prefill_persistent_many_sequences(dev, nh, nkv, d, prefix):
     assert_attn_close(got, prefill_reference(case), what=f"persistent prefill nh={nh} nkv={nkv} d={d} prefix={prefix}")
 
 
+def test_prefill_work_queue_matches_static_order(dev, monkeypatch):
+    """The persistent grid hands items out from a work queue in the workspace
+    the mirror caches per stream, or in a static order without one.  Each item
+    is computed the same way wherever it runs, so the outputs are bit-identical;
+    every call leaves the queue zero, so consecutive calls of different sizes
+    (config 4, a smaller head_dim-64 GQA-7 call, config 4 again) reuse it."""
+    from nanovllm_amd import workloads as W
+    from nanovllm_amd.layers import attention as A
+    gen = torch.Generator().manual_seed(4242)
+    lens = torch.randint(0, 301, (40,), generator=gen).tolist()
+    lens[-1] = 1000
+    pages = sum(-(-(256 + x) // 256) for x in lens) + 4
+    small = W.make_prefill_case(lens, 14, 2, pages, prefix_len=256, head_dim=64, seed=4243, bulk_device=dev,
+                                shared_prefix=False)
+    big = W.config4(dev)
+    orig = A._prefill_workspace
+    for case in (big, small, big):
+        print(f"work queue vs static: {case.name if hasattr(case, 'name') else 'case'}", flush=True)
+        queued = _run_prefill(case)
+        ws = A._PREFILL_WORKSPACES[(dev.index or 0, torch.cuda.current_stream(dev).cuda_stream)]
+        assert int(ws.count_nonzero()) == 0, "the queue must be left zero"
+        monkeypatch.setattr(A, "_prefill_workspace", lambda device, stream: None)
+        static = _run_prefill(case, store=False)
+        monkeypatch.setattr(A, "_prefill_workspace", orig)
+        assert np.array_equal(queued, static)
+        again = _run_prefill(case, store=False)
+        assert np.array_equal(again, queued)
+        assert int(ws.count_nonzero()) == 0
+
+
 @pytest.mark.parametrize("prefix", [0, 256])
 def test_prefill_more_sequences_than_the_persistent_tables(dev, prefix):
     """Over 1024 sequences the persistent grid's tables do not fit its LDS and
