@@ -142,6 +142,27 @@ int nva_decode(const void* q, int64_t q_row_stride,
                void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Gather each sequence's keys and values from the paged caches into packed bf16 rows:
+ * key j of sequence s (block block_table[s*bt_row_stride + j/block_size], j < cu_seqlens_k[s+1] -
+ * cu_seqlens_k[s]) goes to row cu_seqlens_k[s] + j of k_out / v_out.  An fp8 e4m3fn cache is
+ * dequantised (bf16(e4m3 * scale[h]), round to nearest even); a bf16 cache is copied bit for bit.
+ * This is the prefix-cached prefill over an fp8 cache (attention.py:68-73 reads k_cache/v_cache
+ * through block_table): gather, then nva_prefill on the packed rows (block_table NULL).  It has no
+ * single counterpart in the reference, where flash_attn_varlen_func reads the pages itself.
+ * Keys on a block id outside [0, num_blocks) or past max_blocks_per_seq become zero rows; rows at or
+ * beyond out_rows are not written.  max_seqlen_k bounds the launch grid (keys of a sequence beyond
+ * it are not gathered).  head_dim a multiple of 8; out_row_stride a multiple of 8 elements.
+ */
+int nva_gather_kv(const void* k_cache, const void* v_cache, int32_t kv_dtype,
+                  const float* k_scale, const float* v_scale, int64_t num_blocks,
+                  const int32_t* block_table, int64_t bt_row_stride,
+                  int32_t max_blocks_per_seq, int32_t block_size,
+                  const int32_t* cu_seqlens_k, int32_t num_seqs, int32_t max_seqlen_k,
+                  int32_t num_kv_heads, int32_t head_dim,
+                  void* k_out, void* v_out, int64_t out_rows, int64_t out_row_stride,
+                  void* stream);
+
+/*
  * Fused per-head RMSNorm + rotary embedding of q and k: the producer step feeding the
  * path.  Replaces, in Qwen3Attention.forward (qwen3.py:91-105),
  *   q = q_norm(q.view(T, nh, d)); k = k_norm(k.view(T, nkv, d))   layernorm.py:17-27

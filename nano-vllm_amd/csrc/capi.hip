@@ -286,6 +286,55 @@ int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const v
   return hip_status(nva::launch_decode(p, kv_dtype, static_cast<hipStream_t>(stream)), "decode launch");
 }
 
+int nva_gather_kv(const void* k_cache, const void* v_cache, int32_t kv_dtype, const float* k_scale,
+                  const float* v_scale, int64_t num_blocks, const int32_t* block_table, int64_t bt_row_stride,
+                  int32_t max_blocks_per_seq, int32_t block_size, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                  int32_t max_seqlen_k, int32_t num_kv_heads, int32_t head_dim, void* k_out, void* v_out,
+                  int64_t out_rows, int64_t out_row_stride, void* stream) {
+  if (kv_dtype != NVA_DTYPE_BF16 && kv_dtype != NVA_DTYPE_FP8_E4M3)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "unknown kv dtype %d", kv_dtype);
+  if (num_kv_heads <= 0 || head_dim <= 0 || head_dim % 8 != 0)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "num_kv_heads must be positive and head_dim a positive multiple of 8");
+  if (num_seqs < 0 || max_seqlen_k < 0 || out_rows < 0)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "num_seqs, max_seqlen_k and out_rows must be >= 0");
+  if (num_seqs > 65535) return fail(NVA_ERR_UNSUPPORTED, "num_seqs above 65535");
+  if (block_size <= 0 || max_blocks_per_seq <= 0 || bt_row_stride < max_blocks_per_seq || num_blocks <= 0)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "block table shape is inconsistent");
+  const int64_t D = static_cast<int64_t>(num_kv_heads) * head_dim;
+  if (D > (1 << 20)) return fail(NVA_ERR_UNSUPPORTED, "num_kv_heads*head_dim above 2^20");
+  if (out_row_stride < D || out_row_stride % 8)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "out_row_stride must be >= num_kv_heads*head_dim and a multiple of 8");
+  if (num_seqs == 0 || max_seqlen_k == 0 || out_rows == 0) return ok();
+  if (!k_cache || !v_cache || !block_table || !cu_seqlens_k || !k_out || !v_out)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (kv_dtype == NVA_DTYPE_FP8_E4M3 && (!k_scale || !v_scale))
+    return fail(NVA_ERR_INVALID_ARGUMENT, "fp8 kv cache needs k_scale and v_scale");
+  if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(k_out, 16) || !aligned(v_out, 16))
+    return fail(NVA_ERR_INVALID_ARGUMENT, "caches and outputs must be 16-byte aligned");
+  if (!aligned(block_table, 4) || !aligned(cu_seqlens_k, 4))
+    return fail(NVA_ERR_INVALID_ARGUMENT, "index tensors must be 4-byte aligned");
+  nva::GatherParams p{};
+  p.k_cache = k_cache;
+  p.v_cache = v_cache;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.block_table = block_table;
+  p.cu_k = cu_seqlens_k;
+  p.k_out = k_out;
+  p.v_out = v_out;
+  p.bt_row_stride = bt_row_stride;
+  p.num_blocks = num_blocks;
+  p.out_rows = out_rows;
+  p.out_row_stride = out_row_stride;
+  p.max_blocks = max_blocks_per_seq;
+  p.block_size = block_size;
+  p.num_seqs = num_seqs;
+  p.row_elems = static_cast<int32_t>(D);
+  p.head_dim = head_dim;
+  return hip_status(nva::launch_gather_kv(p, max_seqlen_k, kv_dtype, static_cast<hipStream_t>(stream)),
+                    "gather_kv launch");
+}
+
 int nva_qk_norm_rope(const void* q, int64_t q_row_stride, const void* k, int64_t k_row_stride, void* q_out,
                      int64_t q_out_row_stride, void* k_out, int64_t k_out_row_stride, const void* q_norm_weight,
                      const void* k_norm_weight, float eps, const float* cos_sin_cache, int64_t max_position,

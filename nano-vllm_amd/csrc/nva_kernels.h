@@ -96,7 +96,29 @@ struct QKNormRopeParams {
   float eps;
 };
 
+// Paged cache -> packed bf16 rows (gather_kv.hip).
+struct GatherParams {
+  const void* k_cache;        // (num_blocks, block_size, nkv, d) bf16 or fp8
+  const void* v_cache;
+  const float* k_scale;       // [nkv] (fp8) or null
+  const float* v_scale;
+  const int32_t* block_table; // [num_seqs, bt_row_stride]
+  const int32_t* cu_k;        // [num_seqs + 1]
+  void* k_out;                // packed (out_rows, out_row_stride) bf16
+  void* v_out;
+  int64_t bt_row_stride;
+  int64_t num_blocks;
+  int64_t out_rows;
+  int64_t out_row_stride;
+  int32_t max_blocks;
+  int32_t block_size;
+  int32_t num_seqs;
+  int32_t row_elems;          // nkv * d
+  int32_t head_dim;
+};
+
 hipError_t launch_store_kvcache(const StoreParams& p, int vec_bytes, hipStream_t stream);
+hipError_t launch_gather_kv(const GatherParams& p, int max_seqlen_k, int kv_dtype, hipStream_t stream);
 hipError_t launch_qk_norm_rope(const QKNormRopeParams& p, hipStream_t stream);
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, hipStream_t stream);
 hipError_t launch_prefill(const PrefillParams& p, int max_seqlen_q, hipStream_t stream);

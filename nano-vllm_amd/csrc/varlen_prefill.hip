@@ -30,10 +30,13 @@
 // when lane j addresses key row base + j / 4 at dims 4 (j % 4) .. +3, lane i
 // holds dim i of keys base .. base + 3.
 //
-// Softmax runs online in the exp2 domain with a lazily updated row maximum: it
-// moves only when a score exceeds it by more than kTau (so p <= 2^kTau), which
-// makes the rescale of the accumulators rare.  Masks are evaluated only on
-// tiles that cross the causal diagonal or the key end.
+// Softmax runs online in the exp2 domain with a lazily updated row maximum m:
+// Q is scaled by softmax_scale * log2(e) once per item, and every QK chain
+// starts from the accumulator value -m, so the MFMAs deliver s - m directly and
+// each probability is a single exp2.  The first step sets m to the row
+// maximum; after that m moves only when a score exceeds it by more than kTau
+// (so p <= 2^kTau), which makes the rescale of the accumulators rare.  Masks
+// are evaluated only on tiles that cross the causal diagonal or the key end.
 #include <algorithm>
 
 #include "nva_common.h"
@@ -49,7 +52,6 @@ constexpr int kRows = kWaves * kRowsPerWave;  // (position, head) rows per workg
 constexpr int kBK = 64;                       // keys per LDS tile
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kTau = 8.0f;                  // lazy-rescale threshold (log2 units)
-constexpr float kInitMax = -1e30f;            // finite: exp2(fma(s, c, -m)) never sees -inf - -inf
 
 constexpr int kStages = 4;                    // LDS ring depth
 
@@ -129,8 +131,11 @@ __device__ __forceinline__ int page_of(const PrefillParams& p, const_i32* bt, in
 }
 
 // Address of the first key of the 64-key tile at kb: packed K/V from
-// k_start, or the page `page` (paged caches only; a block id outside the pool
-// redirects the tile to slot 0).
+// k_start, or the page `page` (paged caches only).  A block id outside
+// [0, num_blocks) redirects the tile to slot 0, so no access leaves the cache;
+// those keys are not masked (the result of such a sequence is unspecified,
+// other sequences are unaffected).  Masking them costs the loop ~3% (scalar
+// state per ring stage), so only decode masks them.
 template <bool PAGED>
 __device__ __forceinline__ const char* tile_base(const PrefillParams& p, const uint16_t* base, int64_t stride, int page,
                                                  int k_start, int kb) {
@@ -348,7 +353,8 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
   f32x16 acc[NJD];  // O^T, head dims 32 jd + 8 b + 4 h + r of row n
 #pragma unroll
   for (int jd = 0; jd < NJD; ++jd) acc[jd] = f32x16{};
-  float m_run = kInitMax;
+  float m_run = 0.f;  // row maximum (log2 units); scores leave the QK product relative to it
+  f32x16 negm = f32x16{};  // -m_run in every register: the C operand of the QK chain
   float l_run[2] = {0.f, 0.f};  // this lane's half of the row sum, two dot2 chains
   const float sl2 = p.scale_log2;
 
@@ -379,7 +385,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
     for (int ks = 0; ks < NKS; ++ks) kr[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + kaddr[ks]));
   };
   auto qk_mfma = [&](const bf16x8 (&kr)[NKS], f32x16& sacc) {
-    sacc = mfma32x32x16(kr[0], qop[0], f32x16{});
+    sacc = mfma32x32x16(kr[0], qop[0], negm);
 #pragma unroll
     for (int ks = 1; ks < NKS; ++ks) sacc = mfma32x32x16(kr[ks], qop[ks], sacc);
   };
@@ -410,24 +416,26 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
       float mx = sv[0];
 #pragma unroll
       for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sv[i]);
-      mx *= sl2;  // log2 domain (sl2 > 0)
       // Lazy maximum, shared by the two lanes holding a row (n and n + 32): it
       // moves only when a score exceeds it by more than kTau.  Each lane first
       // checks only its own 16 scores; the cross-lane maximum and the rescale
       // run only when some lane exceeds it (the first step, rare outliers).
-      if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau)) {
+      const bool first = key0 == 0;  // the first step sets the maximum
+      if (first || __builtin_amdgcn_ballot_w64(mx > kTau)) {
         mx = max_across_halves(mx);
-        const bool grow = mx > m_run + kTau;  // the same in both lanes of a row
-        const float m_new = grow ? mx : m_run;
-        const float alpha = fast_exp2(m_run - m_new);  // 1 for rows that keep their maximum
+        const bool grow = first ? mx > kNegInf : mx > kTau;  // the same in both lanes of a row
+        const float delta = grow ? mx : 0.f;
+        const float alpha = first ? 1.f : fast_exp2(-delta);  // nothing accumulated before the first step
         l_run[0] *= alpha;
         l_run[1] *= alpha;
 #pragma unroll
         for (int jd = 0; jd < NJD; ++jd) acc[jd] *= alpha;
-        m_run = m_new;
+        m_run += delta;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sv[i] -= delta;
+        negm = f32x16{} - m_run;
       }
       qk_mfma(kr, s_next);
-      const float mneg = -m_run;
       const bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
       bf16x8 pop[2];
 #pragma unroll
@@ -435,8 +443,8 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
         u32x4 pw;
 #pragma unroll
         for (int q2 = 0; q2 < 4; ++q2) {
-          const float a = fast_exp2(__builtin_fmaf(sv[8 * u + 2 * q2], sl2, mneg));
-          const float b = fast_exp2(__builtin_fmaf(sv[8 * u + 2 * q2 + 1], sl2, mneg));
+          const float a = fast_exp2(sv[8 * u + 2 * q2]);
+          const float b = fast_exp2(sv[8 * u + 2 * q2 + 1]);
           // The row sum adds the rounded probabilities the PV product uses,
           // two at a time (v_dot2 against (1, 1)).  The dot2 takes the bf16
           // pair itself: this compiler misselects the register when its
@@ -523,23 +531,27 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
   // operands landed and visible; tile 2's copy starts after the barrier; the
   // first QK is issued
   wait_vmem<0>();
-  // An unconditional use of the Q operands: the compiler's own wait for their
-  // loads lands here.  Its only other use before the loop is conditional, and
+  // Q scaled by softmax_scale * log2(e) once per item: the QK product is then
+  // in the exp2 domain
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    u32x4 wq = as_u32x4(qop[ks]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      wq[j] = pack_bf16x2(__builtin_bit_cast(float, wq[j] << 16) * sl2, __builtin_bit_cast(float, wq[j] & 0xffff0000u) * sl2);
+    qop[ks] = as_bf16x8(wq);
+  }
+  // The scaling above is an unconditional use of the Q operands, so the
+  // compiler's own wait for their loads lands here.  Its only other use before the loop is conditional, and
   // the compiler would then keep those loads pending into the loop and wait
   // for all vector memory there -- which, unknown to it, also drains the tile
   // copies in flight -- on every step.
-#pragma unroll
-  for (int ks = 0; ks < NKS; ++ks) asm volatile("" ::"v"(qop[ks]));
   barrier_lds();
   if (2 < ntiles) {
     stg.template copy_part<0, P>(item, stage(2), c_ptr, 2);
     advance();
   }
   if (0 < wave_kmax) qk(stage(0), s0);
-  // Use the softmax scale (a kernel-argument scalar load) once here, so its
-  // wait lands in the prologue rather than on the first use inside the loop,
-  // where it would also wait for the LDS reads in flight on every step.
-  asm volatile("" ::"s"(sl2));
   // unrolled over the ring's stages, so the stage offsets are immediates
   for (int it0 = 0; it0 < ntiles; it0 += kStages) {
 #pragma unroll

@@ -4,6 +4,8 @@ Public surface, mirroring the reference package layout:
   nanovllm_amd.layers.attention   Attention, store_kvcache, flash_attn_varlen_func,
                                   flash_attn_with_kvcache
   nanovllm_amd.utils.context      Context, get_context, set_context, reset_context
+  nanovllm_amd.engine.kv_cache    allocate_kv_cache (model_runner.py:110-149, + fp8 scales)
+  nanovllm_amd.engine.decode_graphs  DecodeGraphs (model_runner.py:260-336)
 """
 from . import _capi
 from .layers.attention import (Attention, flash_attn_varlen_func, flash_attn_with_kvcache,

@@ -57,6 +57,15 @@ SIGNATURES = {
         _c_void_p, _i64,                   # out, out_row_stride
         _c_void_p, _i64, _c_void_p,        # workspace, workspace_bytes, stream
     ]),
+    "nva_gather_kv": (_i32, [
+        _c_void_p, _c_void_p, _i32,        # k_cache, v_cache, kv_dtype
+        _c_void_p, _c_void_p, _i64,        # k_scale, v_scale, num_blocks
+        _c_void_p, _i64, _i32, _i32,       # block_table, bt_row_stride, max_blocks, block_size
+        _c_void_p, _i32, _i32,             # cu_seqlens_k, num_seqs, max_seqlen_k
+        _i32, _i32,                        # num_kv_heads, head_dim
+        _c_void_p, _c_void_p, _i64, _i64,  # k_out, v_out, out_rows, out_row_stride
+        _c_void_p,                         # stream
+    ]),
     "nva_qk_norm_rope": (_i32, [
         _c_void_p, _i64, _c_void_p, _i64,  # q, q_row_stride, k, k_row_stride
         _c_void_p, _i64, _c_void_p, _i64,  # q_out, q_out_row_stride, k_out, k_out_row_stride

@@ -13,11 +13,13 @@ names and argument meaning, backed by the gfx950 HIP library through its C ABI:
 
 Extension (not in the reference): an fp8 e4m3fn KV cache.  A module whose
 k_cache/v_cache are torch.float8_e4m3fn tensors must also carry k_scale/v_scale
-(float32, one per kv head); store_kvcache then quantises x / scale and decode
-dequantises on the fly.
+(float32, one per kv head; engine/kv_cache.allocate_kv_cache owns and binds
+them); store_kvcache then quantises x / scale, decode dequantises on the fly and a
+prefix-cached prefill gathers the pages into dequantised packed rows first.  A
+prefill without a cached prefix reads the fresh bf16 k/v, as in the reference.
 
 Every launch goes to torch's current stream, nothing synchronises and the only
-allocations are torch tensors (output, decode workspace), so decode can be
+allocations are torch tensors (output, workspaces, fp8 gather rows), so decode can be
 captured in a CUDA/HIP graph as model_runner.py:296-336 does.  There is no
 fallback path: if the library is missing, calls raise.
 """
@@ -58,6 +60,17 @@ def _prefill_workspace(device: torch.device, stream: int) -> torch.Tensor | None
         ws = torch.zeros(int(_capi.load().nva_prefill_workspace_bytes()), dtype=torch.uint8, device=device)
         _PREFILL_WORKSPACES[key] = ws
     return ws
+
+
+def _check_device(device: torch.device, **tensors) -> None:
+    """Every tensor handed to a kernel must live on the GPU the call runs on: a
+    host pointer (or another GPU's) passed through the C ABI would be read by
+    the kernel as a device address."""
+    if device.type != "cuda":
+        raise RuntimeError(f"the attention kernels run on a CUDA (HIP) device, got tensors on {device}")
+    for name, t in tensors.items():
+        if t is not None and t.device != device:
+            raise RuntimeError(f"{name} must be on {device} (got {t.device})")
 
 
 def _cache_dtype_code(cache: torch.Tensor) -> int:
@@ -102,6 +115,8 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
     if _cache_dtype_code(v_cache) != code:
         raise RuntimeError("k_cache and v_cache must share a dtype")
     _check_scales(code, k_scale, v_scale, num_heads, k_cache.device)
+    _check_device(key.device, value=value, k_cache=k_cache, v_cache=v_cache, slot_mapping=slot_mapping,
+                  k_scale=k_scale, v_scale=v_scale)
     num_slots = k_cache.numel() // D
     lib = _capi.load()
     _capi.check(lib.nva_store_kvcache(
@@ -114,14 +129,22 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
 def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, max_seqlen_q: int,
                            cu_seqlens_q: torch.Tensor, max_seqlen_k: int, cu_seqlens_k: torch.Tensor,
                            softmax_scale: float | None = None, causal: bool = True,
-                           block_table: torch.Tensor | None = None) -> torch.Tensor:
+                           block_table: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
+                           v_scale: torch.Tensor | None = None) -> torch.Tensor:
     """Varlen causal attention over packed K/V, or over the paged caches when
-    block_table is given (attention.py:67-73).  q (total_q, nh, d) -> (total_q, nh, d)."""
+    block_table is given (attention.py:67-73).  q (total_q, nh, d) -> (total_q, nh, d).
+
+    Extension: paged caches in fp8 e4m3fn (with k_scale/v_scale, one float32 per
+    kv head) are first gathered into packed bf16 rows, dequantised
+    (nva_gather_kv), and the packed prefill runs on those.  That needs
+    cu_seqlens_k[s+1] - cu_seqlens_k[s] <= max_seqlen_k, as flash-attn does."""
     if not causal:
         raise RuntimeError("only causal=True is implemented (the only mode attention.py uses)")
     total_q, nh, d = q.shape
-    if q.dtype != _BF16 or k.dtype != _BF16 or v.dtype != _BF16:
-        raise RuntimeError("q/k/v must be bfloat16 (an fp8 cache is read by decode only)")
+    if q.dtype != _BF16:
+        raise RuntimeError("q must be bfloat16")
+    if block_table is None and (k.dtype != _BF16 or v.dtype != _BF16):
+        raise RuntimeError("packed k/v must be bfloat16 (an fp8 cache is read through block_table)")
     if softmax_scale is None:
         softmax_scale = d ** -0.5
     if q.stride(-1) != 1 or q.stride(1) != d:
@@ -136,17 +159,41 @@ def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ma
     if block_table is not None:
         if k.dim() != 4 or not k.is_contiguous() or not v.is_contiguous() or k.shape != v.shape:
             raise RuntimeError("paged k/v must be contiguous (num_blocks, block_size, nkv, d) caches")
-        num_blocks, block_size, nkv, _ = k.shape
-        if block_table.dtype != torch.int32 or block_table.stride(-1) != 1:
-            raise RuntimeError("block_table must be int32 with unit column stride")
+        num_blocks, block_size, nkv, kd = k.shape
+        if kd != d:
+            raise RuntimeError(f"cache head_dim {kd} differs from q's {d}")
+        if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(-1) != 1:
+            raise RuntimeError("block_table must be a 2-d int32 tensor with unit column stride")
+        if block_table.shape[0] != num_seqs:
+            raise RuntimeError(f"block_table has {block_table.shape[0]} rows for {num_seqs} sequences")
+        code = _cache_dtype_code(k)
+        if _cache_dtype_code(v) != code:
+            raise RuntimeError("k_cache and v_cache must share a dtype")
+        _check_scales(code, k_scale, v_scale, nkv, k.device)
         k_row = v_row = nkv * d
         bt_ptr, bt_stride, max_blocks = block_table.data_ptr(), block_table.stride(0), block_table.shape[1]
+        if code == _capi.NVA_DTYPE_FP8_E4M3:
+            # dequantise each sequence's pages into packed rows, then the packed prefill
+            _check_device(q.device, k=k, v=v, cu_seqlens_k=cu_seqlens_k, block_table=block_table,
+                          k_scale=k_scale, v_scale=v_scale)
+            rows = num_seqs * int(max_seqlen_k)
+            kp = torch.empty((rows, nkv, d), dtype=_BF16, device=q.device)
+            vp = torch.empty((rows, nkv, d), dtype=_BF16, device=q.device)
+            _capi.check(_capi.load().nva_gather_kv(
+                k.data_ptr(), v.data_ptr(), code, _ptr(k_scale), _ptr(v_scale), num_blocks,
+                bt_ptr, bt_stride, max_blocks, block_size, cu_seqlens_k.data_ptr(), num_seqs, int(max_seqlen_k),
+                nkv, d, kp.data_ptr(), vp.data_ptr(), rows, nkv * d, _stream(q)))
+            k, v, block_table = kp, vp, None
+            bt_ptr, bt_stride, max_blocks, block_size, num_blocks = None, 0, 0, 0, 0
     else:
-        if k.dim() != 3 or k.stride(-1) != 1 or v.stride(-1) != 1 or k.stride(1) != d or v.stride(1) != d:
-            raise RuntimeError("packed k/v must be (total_k, nkv, d) with head stride d")
+        if k.dim() != 3 or k.shape != v.shape or k.shape[2] != d:
+            raise RuntimeError("packed k/v must both be (total_k, nkv, d) with q's head_dim")
+        if k.stride(-1) != 1 or v.stride(-1) != 1 or k.stride(1) != d or v.stride(1) != d:
+            raise RuntimeError("packed k/v must have head stride d and unit element stride")
         nkv = k.shape[1]
         k_row, v_row = k.stride(0), v.stride(0)
         bt_ptr, bt_stride, max_blocks, block_size, num_blocks = None, 0, 0, 0, 0
+    _check_device(q.device, k=k, v=v, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k, block_table=block_table)
     lib = _capi.load()
     stream = _stream(q)
     ws = _prefill_workspace(q.device, stream)
@@ -180,7 +227,9 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
         softmax_scale = d ** -0.5
     if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise RuntimeError("caches must be contiguous (num_blocks, block_size, nkv, d) of one shape")
-    num_blocks, block_size, nkv, _ = k_cache.shape
+    num_blocks, block_size, nkv, kd = k_cache.shape
+    if kd != d:
+        raise RuntimeError(f"cache head_dim {kd} differs from q's {d}")
     code = _cache_dtype_code(k_cache)
     if _cache_dtype_code(v_cache) != code:
         raise RuntimeError("k_cache and v_cache must share a dtype")
@@ -190,6 +239,8 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     if block_table.dtype != torch.int32 or block_table.stride(-1) != 1 or block_table.shape[0] != B:
         raise RuntimeError("block_table must be int32 (batch, max_blocks) with unit column stride")
     max_blocks = block_table.shape[1]
+    _check_device(q.device, k_cache=k_cache, v_cache=v_cache, cache_seqlens=cache_seqlens, block_table=block_table,
+                  k_scale=k_scale, v_scale=v_scale)
     out = torch.empty((B, 1, nh, d), dtype=_BF16, device=q.device)
     lib = _capi.load()
     ws_bytes = lib.nva_decode_workspace_bytes(B, nh, nkv, d, max_blocks, block_size, code, int(num_splits))
@@ -230,7 +281,8 @@ class Attention(nn.Module):
             o = flash_attn_varlen_func(q, k, v,
                                        max_seqlen_q=context.max_seqlen_q, cu_seqlens_q=context.cu_seqlens_q,
                                        max_seqlen_k=context.max_seqlen_k, cu_seqlens_k=context.cu_seqlens_k,
-                                       softmax_scale=self.scale, causal=True, block_table=context.block_tables)
+                                       softmax_scale=self.scale, causal=True, block_table=context.block_tables,
+                                       k_scale=self.k_scale, v_scale=self.v_scale)
         else:  # decode
             o = flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
                                         cache_seqlens=context.context_lens, block_table=context.block_tables,

@@ -91,6 +91,11 @@ class PrefillCase:
     seed: int = 0
     lens_q: list = field(default_factory=list)
     lens_k: list = field(default_factory=list)
+    # the pages the scheduler allocated to each sequence (model_runner.py:151-159),
+    # -1 padded, kept on the host whether or not a prefix is cached, and the
+    # cached tokens of each sequence: the inputs of the slot formula
+    page_table: torch.Tensor | None = None
+    prefix_lens: list = field(default_factory=list)
 
     def flops(self) -> int:
         pairs = sum(lq * (lk - lq) + lq * (lq + 1) // 2 for lq, lk in zip(self.lens_q, self.lens_k))
@@ -114,7 +119,8 @@ class PrefillCase:
                            self.scale, mv(self.q), mv(self.k), v, mv(self.cu_seqlens_q),
                            mv(self.cu_seqlens_k), self.max_seqlen_q, self.max_seqlen_k,
                            mv(self.slot_mapping), mv(self.k_cache), mv(self.v_cache),
-                           mv(self.block_tables), self.seed, list(self.lens_q), list(self.lens_k))
+                           mv(self.block_tables), self.seed, list(self.lens_q), list(self.lens_k),
+                           self.page_table, list(self.prefix_lens))
 
 
 def _randn_bf16(shape, gen, device):
@@ -185,11 +191,15 @@ def make_decode_case(batch, num_heads, num_kv_heads, ctx_lo, ctx_hi, num_blocks,
             slots[b] = row[pages[b] - 1] * block_size + last - 1
         else:
             slots[b] = -1
+    q = k_new = v_new = k_cache = v_cache = k_scale = v_scale = None
+    if bulk_device is None:  # the index tensors only (lengths, block tables, slots)
+        return DecodeCase(name, num_heads, num_kv_heads, head_dim, block_size, head_dim ** -0.5, q, k_new, v_new,
+                          k_cache, v_cache, torch.tensor(lengths, dtype=torch.int32), bt, slots, None, None, seed,
+                          list(lengths))
     g = _bulk_gen(seed, bulk_device)
     q, k_new, v_new = _qkv_views(batch, num_heads, num_kv_heads, head_dim, g, bulk_device)
     k_cache = _fill_cache(num_blocks, block_size, num_kv_heads, head_dim, g, bulk_device)
     v_cache = _fill_cache(num_blocks, block_size, num_kv_heads, head_dim, g, bulk_device)
-    k_scale = v_scale = None
     if fp8:
         # the scale's amax covers every source value that enters the cache,
         # including the newest token, so x / scale never exceeds 448
@@ -204,24 +214,33 @@ def make_decode_case(batch, num_heads, num_kv_heads, ctx_lo, ctx_hi, num_blocks,
 def make_prefill_case(lens_q, num_heads, num_kv_heads, num_blocks, *, prefix_len=0, block_size=256,
                       head_dim=128, seed=0, bulk_device="cpu", name="prefill", shared_prefix=True,
                       gen=None) -> PrefillCase:
-    """lens_q: fresh tokens per sequence.  prefix_len > 0: that many cached
-    tokens (a multiple of block_size) precede every sequence, in pages shared by
-    all sequences when shared_prefix, already present in the cache."""
-    if prefix_len % block_size:
+    """lens_q: fresh tokens per sequence.  prefix_len (an int, or one value per
+    sequence): that many cached tokens, whole pages (block_manager.py:74),
+    precede the sequence's fresh ones and are already in the cache.  With
+    shared_prefix the cached pages are common to all sequences (a sequence with
+    a shorter prefix uses the first of them).  Whenever any sequence has a
+    cached prefix the whole batch gets block tables and takes the paged path,
+    as model_runner.py:189-190 sets them; a sequence without one then reads all
+    its keys back from the pages the store just wrote."""
+    S = len(lens_q)
+    pre_lens = list(prefix_len) if isinstance(prefix_len, (list, tuple)) else [prefix_len] * S
+    if len(pre_lens) != S:
+        raise ValueError("one prefix length per sequence")
+    if any(x % block_size for x in pre_lens):
         raise ValueError("a cached prefix is whole pages (block_manager.py:74)")
     gen = gen or torch.Generator().manual_seed(seed)
-    S = len(lens_q)
-    lens_k = [prefix_len + x for x in lens_q]
+    lens_k = [pre + x for pre, x in zip(pre_lens, lens_q)]
     perm = torch.randperm(num_blocks, generator=gen).tolist()
     at = 0
-    pre_pages = prefix_len // block_size
-    shared = perm[:pre_pages] if shared_prefix else None
+    max_pre_pages = max(pre_lens, default=0) // block_size
+    shared = perm[:max_pre_pages] if shared_prefix else None
     if shared_prefix:
-        at = pre_pages
+        at = max_pre_pages
     rows = []
     for s in range(S):
+        pre_pages = pre_lens[s] // block_size
         if shared_prefix:
-            pre = list(shared)
+            pre = list(shared[:pre_pages])
         else:
             pre = perm[at:at + pre_pages]
             at += pre_pages
@@ -230,30 +249,33 @@ def make_prefill_case(lens_q, num_heads, num_kv_heads, num_blocks, *, prefix_len
         at += n_new
     if at > num_blocks:
         raise ValueError(f"{at} pages needed, pool has {num_blocks}")
-    width = max(len(r) for r in rows)
-    bt = torch.full((S, width), -1, dtype=torch.int32)
+    width = max((len(r) for r in rows), default=1)
+    bt = torch.full((S, max(width, 1)), -1, dtype=torch.int32)
     slots = []
     for s, r in enumerate(rows):
         bt[s, :len(r)] = torch.tensor(r, dtype=torch.int32)
         nb = len(r)
-        for i in range(pre_pages, nb):
+        for i in range(pre_lens[s] // block_size, nb):
             start = r[i] * block_size
             end = start + (block_size if i != nb - 1 else lens_k[s] - (nb - 1) * block_size)
             slots.extend(range(start, end))
     T = sum(lens_q)
-    g = _bulk_gen(seed, bulk_device)
-    q, k, v = _qkv_views(T, num_heads, num_kv_heads, head_dim, g, bulk_device)
-    k_cache = _fill_cache(num_blocks, block_size, num_kv_heads, head_dim, g, bulk_device)
-    v_cache = _fill_cache(num_blocks, block_size, num_kv_heads, head_dim, g, bulk_device)
+    q = k = v = k_cache = v_cache = None
+    if bulk_device is not None:  # None: the index tensors only
+        g = _bulk_gen(seed, bulk_device)
+        q, k, v = _qkv_views(T, num_heads, num_kv_heads, head_dim, g, bulk_device)
+        k_cache = _fill_cache(num_blocks, block_size, num_kv_heads, head_dim, g, bulk_device)
+        v_cache = _fill_cache(num_blocks, block_size, num_kv_heads, head_dim, g, bulk_device)
     cu_q = torch.zeros(S + 1, dtype=torch.int32)
     cu_k = torch.zeros(S + 1, dtype=torch.int32)
     cu_q[1:] = torch.cumsum(torch.tensor(lens_q), 0)
     cu_k[1:] = torch.cumsum(torch.tensor(lens_k), 0)
-    dev = bulk_device
+    dev = bulk_device or "cpu"
     return PrefillCase(name, num_heads, num_kv_heads, head_dim, block_size, head_dim ** -0.5, q, k, v,
                        cu_q.to(dev), cu_k.to(dev), max(lens_q) if S else 0, max(lens_k) if S else 0,
                        torch.tensor(slots, dtype=torch.int32, device=dev), k_cache, v_cache,
-                       bt.to(dev) if prefix_len > 0 else None, seed, list(lens_q), list(lens_k))
+                       bt.to(dev) if any(pre_lens) else None, seed, list(lens_q), list(lens_k),
+                       bt.clone(), list(pre_lens))
 
 
 # ----------------------------------------------------------------------------

@@ -1,6 +1,7 @@
 """The decode graph harness (nanovllm_amd.engine.decode_graphs) on the GPU: captured
-steps of two Attention layers replayed at several batch sizes match eager
-execution, padded rows leave the cache alone (slot pad -1, reference quirk Q1),
+steps of two Attention layers replayed at several batch sizes match the CPU oracle
+on the caches as the replay left them (and eager execution), the padded rows of a
+graph produce zeros and leave the cache alone (slot pad -1, reference quirk Q1),
 and sizes beyond the largest graph run eagerly."""
 from __future__ import annotations
 
@@ -10,7 +11,9 @@ import numpy as np
 import pytest
 import torch
 
-from _helpers import assert_attn_close, f32
+from types import SimpleNamespace
+
+from _helpers import assert_attn_close, bits16, decode_reference, f32
 
 pytestmark = pytest.mark.gpu
 
@@ -67,6 +70,14 @@ def _eager(layers, q, k, v, slots, ctx, bt):
         nva.reset_context()
 
 
+def _oracle(layer, q, ctx, bt):
+    """Oracle decode of one layer on its cache as it is now (after the step's store)."""
+    case = SimpleNamespace(batch=q.shape[0], context_lens=ctx, block_tables=bt, q=q.view(-1, NH, D),
+                           num_heads=NH, num_kv_heads=NKV, head_dim=D, block_size=BS_PAGE, scale=D ** -0.5,
+                           k_cache=layer.k_cache, v_cache=layer.v_cache, k_scale=None, v_scale=None)
+    return decode_reference(case)
+
+
 def test_replay_matches_eager_and_skips_padding(dev):
     from nanovllm_amd.engine.decode_graphs import DecodeGraphs
     max_blocks, num_blocks = 4, 160
@@ -81,12 +92,25 @@ def test_replay_matches_eager_and_skips_padding(dev):
         a.v_cache[0, 0].fill_(-7.0)
     graphs = DecodeGraphs(layers, max_bs=48, max_num_blocks=max_blocks).capture()
     assert sorted(graphs.graphs) == [1, 2, 4, 8, 16, 32, 48]
-    for i, bs in enumerate([1, 3, 16, 17, 40, 48]):
+    # graphs 1, 4, 16, 32 and 48 replayed, 48 and 1 twice, with eager work between
+    for i, bs in enumerate([1, 3, 16, 17, 40, 48, 2, 1]):
         batch = _batch(dev, bs, max_blocks - 1, num_blocks, seed=100 + i)
         got = torch.stack(graphs.run(*batch))
-        ref = _eager(twins, *batch)
         torch.cuda.synchronize()
         assert got.shape == (2, bs, NH * D)
+        q, _, _, slots, ctx, bt = batch
+        for li, a in enumerate(layers):
+            # the new token is in its slot, and the replay equals the oracle on that cache
+            assert np.array_equal(bits16(a.k_cache.view(-1, NKV * D)[slots.long()]), bits16(batch[1]))
+            assert np.array_equal(bits16(a.v_cache.view(-1, NKV * D)[slots.long()]), bits16(batch[2]))
+            assert_attn_close(f32(got[li]).reshape(bs, NH, D), _oracle(a, q, ctx, bt),
+                              what=f"graph bs={bs} layer {li} vs oracle")
+        # rows of the graph beyond bs ran with zero context: zeros
+        size = min(x for x in graphs.graph_bs if x >= bs)
+        for out in graphs.layer_outputs[size]:
+            assert not bool(out[bs:size].any())
+        ref = _eager(twins, *batch)
+        torch.cuda.synchronize()
         # the padded launch plans its split-K for the graph size, so sums may round differently
         assert_attn_close(f32(got), f32(ref), what=f"graph bs={bs}")
         for a, t in zip(layers, twins):  # same cache contents: the live rows' store
