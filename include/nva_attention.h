@@ -163,6 +163,30 @@ int nva_gather_kv(const void* k_cache, const void* v_cache, int32_t kv_dtype,
                   void* stream);
 
 /*
+ * nva_decode without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP-graph capture, tight serving loops, harnesses that forbid hipMalloc).  It has
+ * no counterpart in the reference.  Same arguments, checks and results as nva_decode (the same
+ * kernels, bit for bit); the split-K partials live in a static __device__ array of the library
+ * (nva_decode_noalloc_max_workspace_bytes() bytes, 32 MiB, on each GPU the library runs on,
+ * held until the process ends).  A call whose nva_decode_workspace_bytes exceeds that size is
+ * refused with NVA_ERR_WORKSPACE before any HIP call.  Nothing is allocated or freed, and nothing
+ * in the array needs to start at zero.  Every call on one GPU shares that GPU's array: calls
+ * that can overlap on one GPU (different streams, or a graph replay concurrent with another
+ * call) race and must not be issued.
+ */
+int nva_decode_noalloc(const void* q, int64_t q_row_stride,
+                       const void* k_cache, const void* v_cache, int32_t kv_dtype,
+                       const float* k_scale, const float* v_scale, int64_t num_blocks,
+                       const int32_t* cache_seqlens, const int32_t* block_table,
+                       int64_t bt_row_stride, int32_t max_blocks_per_seq, int32_t block_size,
+                       int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                       float softmax_scale, int32_t num_splits,
+                       void* out, int64_t out_row_stride, void* stream);
+
+/* Size in bytes of nva_decode_noalloc's static scratch (the largest workspace it serves). */
+int64_t nva_decode_noalloc_max_workspace_bytes(void);
+
+/*
  * Fused per-head RMSNorm + rotary embedding of q and k: the producer step feeding the
  * path.  Replaces, in Qwen3Attention.forward (qwen3.py:91-105),
  *   q = q_norm(q.view(T, nh, d)); k = k_norm(k.view(T, nkv, d))   layernorm.py:17-27

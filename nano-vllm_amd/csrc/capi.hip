@@ -4,10 +4,14 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 
 #include "nva_attention.h"
 #include "nva_kernels.h"
+
+// The static decode scratch of nva_decode_noalloc (see scratch_on_current_device).
+static __device__ __align__(256) char scratch[nva::kDecodeScratchBytes];
 
 namespace {
 
@@ -198,12 +202,53 @@ int64_t nva_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num
   return (bytes + 255) & ~static_cast<int64_t>(255);
 }
 
-int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache, int32_t kv_dtype,
-               const float* k_scale, const float* v_scale, int64_t num_blocks, const int32_t* cache_seqlens,
-               const int32_t* block_table, int64_t bt_row_stride, int32_t max_blocks_per_seq, int32_t block_size,
-               int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
-               int32_t num_splits, void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
-               void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Static decode scratch for nva_decode_noalloc: device memory of the library
+// itself, so that entry point allocates nothing.  Each GPU holds its own copy
+// of the array until the process ends; its device address on the current GPU
+// is looked up once per device (hipGetSymbolAddress) and kept.  In host code
+// the name `scratch` is only a host-side stand-in: kernels get the looked-up
+// address, never the name.
+constexpr int64_t kDecodeScratchBytes = nva::kDecodeScratchBytes;
+
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+char g_scratch_error[256] = "";
+
+void* scratch_on_current_device() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    snprintf(g_scratch_error, sizeof(g_scratch_error), "hipGetDevice: %s (device %d)", hipGetErrorString(e), dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      snprintf(g_scratch_error, sizeof(g_scratch_error), "hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+// nva_decode's body.  `scratch_max` > 0 selects the no-allocation variant: the
+// workspace is the library's static scratch array (`workspace` its device
+// address, fetched lazily by `get_scratch` once the arguments are valid) and a
+// launch that needs more than scratch_max bytes is refused before any HIP call.
+int decode_impl(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache, int32_t kv_dtype,
+                const float* k_scale, const float* v_scale, int64_t num_blocks, const int32_t* cache_seqlens,
+                const int32_t* block_table, int64_t bt_row_stride, int32_t max_blocks_per_seq, int32_t block_size,
+                int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
+                int32_t num_splits, void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+                void* stream, int64_t scratch_max, void* (*get_scratch)()) {
   if (head_dim != 128 && head_dim != 64)
     return fail(NVA_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", head_dim);
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
@@ -247,6 +292,16 @@ int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const v
       nva::plan_decode(batch, num_kv_heads, max_blocks_per_seq, block_size, kv_dtype, num_splits);
   const int64_t need = nva_decode_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
                                                   block_size, kv_dtype, num_splits);
+  if (scratch_max > 0) {
+    if (need > scratch_max)
+      return fail(NVA_ERR_WORKSPACE,
+                  "decode needs %lld bytes of workspace, above the %lld-byte static scratch of nva_decode_noalloc "
+                  "(use nva_decode with a caller-allocated workspace)",
+                  (long long)need, (long long)scratch_max);
+    workspace = need > 0 ? get_scratch() : nullptr;
+    if (need > 0 && !workspace) return fail(NVA_ERR_HIP, "static decode scratch unavailable: %s", g_scratch_error);
+    workspace_bytes = scratch_max;
+  }
   if (need > 0) {
     if (!workspace || workspace_bytes < need)
       return fail(NVA_ERR_WORKSPACE, "decode needs a workspace of %lld bytes (got %lld)", (long long)need,
@@ -284,6 +339,36 @@ int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const v
   p.head_dim = head_dim;
   p.scale_log2 = softmax_scale * kLog2e;
   return hip_status(nva::launch_decode(p, kv_dtype, static_cast<hipStream_t>(stream)), "decode launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache, int32_t kv_dtype,
+               const float* k_scale, const float* v_scale, int64_t num_blocks, const int32_t* cache_seqlens,
+               const int32_t* block_table, int64_t bt_row_stride, int32_t max_blocks_per_seq, int32_t block_size,
+               int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
+               int32_t num_splits, void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+               void* stream) {
+  return decode_impl(q, q_row_stride, k_cache, v_cache, kv_dtype, k_scale, v_scale, num_blocks, cache_seqlens,
+                     block_table, bt_row_stride, max_blocks_per_seq, block_size, batch, num_heads, num_kv_heads,
+                     head_dim, softmax_scale, num_splits, out, out_row_stride, workspace, workspace_bytes, stream, 0,
+                     nullptr);
+}
+
+int64_t nva_decode_noalloc_max_workspace_bytes(void) { return kDecodeScratchBytes; }
+
+int nva_decode_noalloc(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                       int32_t kv_dtype, const float* k_scale, const float* v_scale, int64_t num_blocks,
+                       const int32_t* cache_seqlens, const int32_t* block_table, int64_t bt_row_stride,
+                       int32_t max_blocks_per_seq, int32_t block_size, int32_t batch, int32_t num_heads,
+                       int32_t num_kv_heads, int32_t head_dim, float softmax_scale, int32_t num_splits, void* out,
+                       int64_t out_row_stride, void* stream) {
+  return decode_impl(q, q_row_stride, k_cache, v_cache, kv_dtype, k_scale, v_scale, num_blocks, cache_seqlens,
+                     block_table, bt_row_stride, max_blocks_per_seq, block_size, batch, num_heads, num_kv_heads,
+                     head_dim, softmax_scale, num_splits, out, out_row_stride, nullptr, 0, stream,
+                     kDecodeScratchBytes, scratch_on_current_device);
 }
 
 int nva_gather_kv(const void* k_cache, const void* v_cache, int32_t kv_dtype, const float* k_scale,

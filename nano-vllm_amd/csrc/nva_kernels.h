@@ -129,6 +129,8 @@ constexpr int kPrefillMaxGroup = 256;        // rows per prefill workgroup bound
 constexpr int kPrefillQueueLanes = 8;
 constexpr int kPrefillQueueWords = kPrefillQueueLanes + 1;
 constexpr int64_t kPrefillWorkspaceBytes = 256;
+// Static device scratch of nva_decode_noalloc (bytes, per GPU).
+constexpr int64_t kDecodeScratchBytes = int64_t{32} << 20;
 static_assert(kPrefillQueueWords * 4 <= kPrefillWorkspaceBytes, "queue fits the workspace");
 
 // Split-K plan shared by nva_decode and nva_decode_workspace_bytes.

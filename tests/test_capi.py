@@ -215,3 +215,20 @@ def test_qk_norm_rope_zero_tokens_is_noop(lib):
 def test_decode_refuses_fp8_head_dim_64(lib):
     assert decode(lib, head_dim=64, kv_dtype=1, k_scale=A, v_scale=B) == _capi.NVA_ERR_UNSUPPORTED
     assert "head_dim" in lib.nva_last_error().decode()
+
+
+def test_decode_noalloc_refuses_above_its_scratch(lib):
+    """nva_decode_noalloc serves workspaces up to its static scratch and refuses a
+    larger one with NVA_ERR_WORKSPACE before any HIP call (so this runs without a
+    GPU)."""
+    cap = lib.nva_decode_noalloc_max_workspace_bytes()
+    assert cap == 32 << 20
+    assert lib.nva_decode_workspace_bytes(4096, 128, 8, 128, 64, 256, 0, 8) > cap
+    rc = lib.nva_decode_noalloc(A, 128 * 128, B, C, 0, None, None, 100, A + 0x8000, A + 0x9000, 64, 64, 256, 4096,
+                                128, 8, 128, 0.1, 8, B + 0x40000, 128 * 128, None)
+    assert rc == _capi.NVA_ERR_WORKSPACE
+    assert b"static scratch" in lib.nva_last_error()
+    # argument checks run first, as in nva_decode
+    rc = lib.nva_decode_noalloc(A, 128, B, C, 0, None, None, 100, A, A, 64, 64, 256, 4, 16, 8, 96, 0.1, 0,
+                                B, 128, None)
+    assert rc == _capi.NVA_ERR_UNSUPPORTED
