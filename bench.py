@@ -7,8 +7,12 @@ context U[100, 2048], 2048-page pool).  A step is one such pass with inputs
 resident in HBM; consecutive steps alternate between independent cache pools so
 the 256 MB Infinity Cache cannot serve them.  Alongside: prefill TFLOP/s
 (config 4 prefix-cached, Qwen3-8B heads 32/8; config 2 varlen), fp8-KV decode
-GB/s (config 5), the fused qk-RMSNorm + rotary producer step (GB/s), the roofline of the dominant kernel (HIP events on the launch
-stream) and the PyTorch CPU baseline (gather + SDPA) on the host cores.
+GB/s (config 5), the config 1 decode step (cache-resident, reported without a
+roofline claim), the fused qk-RMSNorm + rotary producer step (GB/s), the captured
+decode steps, the roofline of the dominant kernel (HIP events on the launch
+stream), rocprofv3 HBM traffic from profiles/, and the reference's PyTorch CPU
+path (store + gather + SDPA) timed on the host cores on a bounded sample of
+every configuration (`cpu_baseline` is config 3's, `cpu_baselines` all five).
 
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--warm-seconds 1] [--no-cpu]
                        [--only decode|prefill|fp8|producer|graphs]
@@ -35,10 +39,10 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def profiled_traffic(key: str):
+def profiled_traffic(key: str, summary: str = "decode_hbm_traffic.md"):
     """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (scaled by a
     plain copy of known size), as recorded in the committed profile summary."""
-    path = ROOT / "profiles" / "decode_hbm_traffic.md"
+    path = ROOT / "profiles" / summary
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -249,39 +253,94 @@ def bench_graph_decode(dev, steps, warmup, warm_s=1.0, layers=28, ctx=1024, batc
     return res
 
 
-def cpu_baseline_decode(case_gpu, budget_s=20.0):
-    """Reference-semantics PyTorch CPU decode step on a bounded sample of config 3."""
-    import torch
-    sys.path.insert(0, str(ROOT))
-    from oracle import cpu_baseline as CB
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
-    case = case_gpu.to("cpu")
-    B = case.batch
-    # sample: the first n sequences, n chosen from a one-sequence probe so the
-    # timed work stays within the budget
-    t0 = time.perf_counter()
-    CB.decode(case.q[:8], case.k_cache, case.v_cache, case.context_lens[:8], case.block_tables[:8], case.scale)
-    per_seq = (time.perf_counter() - t0) / 8
-    n = max(8, min(B, int(budget_s / 3 / max(per_seq, 1e-6))))
-    # then repeat the sample (the store rewrites the same slots with the same
-    # rows) until about half the budget has been spent, at least 3 times
+def _cpu_time(fn, budget_s):
+    """Median wall time of fn() on the host, repeated until about half the budget
+    is spent (at least 3 runs); returns (seconds, runs)."""
     times = []
     t_start = time.perf_counter()
     while len(times) < 3 or (time.perf_counter() - t_start < budget_s / 2 and len(times) < 500):
         t0 = time.perf_counter()
-        CB.store_kvcache(case.k_new[:n], case.v_new[:n], case.k_cache, case.v_cache, case.slot_mapping[:n])
-        CB.decode(case.q[:n], case.k_cache, case.v_cache, case.context_lens[:n], case.block_tables[:n], case.scale)
+        fn()
         times.append(time.perf_counter() - t0)
-    reps = len(times)
-    t = sorted(times)[len(times) // 2]
+    return sorted(times)[len(times) // 2], len(times)
+
+
+def _decode_bytes(case, n):
+    """Algorithmic bytes of a decode step (store of the new token + attention) over
+    the first n sequences of a decode case."""
     L = sum(case.lengths[:n])
     D = case.num_kv_heads * case.head_dim
-    bytes_ = L * D * 2 * 2 + n * case.num_heads * case.head_dim * 2 * 2 + 4 * n
-    bytes_ += 4 * sum(math.ceil(x / case.block_size) for x in case.lengths[:n]) + 2 * n * D * 2 * 2
-    return dict(value=bytes_ / t / 1e9, unit="GB/s", cores=threads, kind="port",
-                sample=f"config-3 decode step (index_copy_ store + block-table gather + SDPA, bf16) "
-                       f"over the first {n} of {B} sequences, median of {reps}, {t:.2f} s each")
+    elem = case.k_cache.element_size()
+    b = L * D * 2 * elem + n * case.num_heads * case.head_dim * 2 * 2 + 4 * n
+    b += 4 * sum(math.ceil(x / case.block_size) for x in case.lengths[:n])
+    return b + 2 * n * D * 2 + 2 * n * D * elem
+
+
+def cpu_baseline_decode(case, name, budget_s):
+    """Reference-semantics PyTorch CPU decode step (store + gather + SDPA; fp8 pages
+    dequantised per sequence) on the first n sequences of a host copy of `case`, n
+    chosen from a probe so the timed work fits the budget."""
+    import torch
+    sys.path.insert(0, str(ROOT))
+    from oracle import cpu_baseline as CB
+    B = case.batch
+    kw = dict(k_scale=case.k_scale, v_scale=case.v_scale)
+    fp8 = case.k_scale is not None
+    kc, vc = case.k_cache, case.v_cache
+    if fp8:  # the byte copies of the store go through uint8 views of the same memory
+        kc, vc = kc.view(torch.uint8), vc.view(torch.uint8)
+    probe = min(B, 2 if fp8 else 8)
+    t0 = time.perf_counter()
+    CB.decode(case.q[:probe], case.k_cache, case.v_cache, case.context_lens[:probe], case.block_tables[:probe],
+              case.scale, **kw)
+    per_seq = (time.perf_counter() - t0) / probe
+    n = max(probe, min(B, int(budget_s / 3 / max(per_seq, 1e-6))))
+
+    def step():
+        k_new, v_new = case.k_new[:n], case.v_new[:n]
+        if fp8:  # the fp8 store: e4m3fn(x / scale), torch's cast (bit-identical to the kernel's)
+            k_new = (k_new.float() / case.k_scale.view(1, -1, 1)).to(torch.float8_e4m3fn).view(torch.uint8)
+            v_new = (v_new.float() / case.v_scale.view(1, -1, 1)).to(torch.float8_e4m3fn).view(torch.uint8)
+        CB.store_kvcache(k_new, v_new, kc, vc, case.slot_mapping[:n])
+        CB.decode(case.q[:n], case.k_cache, case.v_cache, case.context_lens[:n], case.block_tables[:n],
+                  case.scale, **kw)
+
+    t, reps = _cpu_time(step, budget_s)
+    what = "fp8 e4m3fn decode step (store + gather + dequantise + SDPA)" if fp8 else \
+        "decode step (index_copy_ store + block-table gather + SDPA, bf16)"
+    return dict(value=round(_decode_bytes(case, n) / t / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(),
+                kind="port", sample=f"{name} {what} over the first {n} of {B} sequences, median of {reps}, "
+                                    f"{t:.3f} s each")
+
+
+def cpu_baseline_prefill(case, name, budget_s):
+    """Reference-semantics PyTorch CPU prefill (store + per-sequence SDPA with a
+    bottom-right causal mask; prefix pages gathered through the block table) over
+    the first n sequences of a host copy of `case`."""
+    import torch
+    sys.path.insert(0, str(ROOT))
+    from oracle import cpu_baseline as CB
+    S = len(case.lens_q)
+    paged = case.block_tables is not None
+
+    def run(n):
+        T = sum(case.lens_q[:n])
+        CB.store_kvcache(case.k[:T], case.v[:T], case.k_cache, case.v_cache, case.slot_mapping[:T])
+        k, v = (case.k_cache, case.v_cache) if paged else (case.k, case.v)
+        CB.prefill(case.q[:T], k, v, case.cu_seqlens_q[:n + 1], case.cu_seqlens_k[:n + 1], case.scale,
+                   case.block_tables[:n] if paged else None)
+
+    t0 = time.perf_counter()
+    run(1)
+    per_seq = time.perf_counter() - t0
+    n = max(1, min(S, int(budget_s / 3 / max(per_seq, 1e-6))))
+    t, reps = _cpu_time(lambda: run(n), budget_s)
+    flops = sum(4 * case.head_dim * case.num_heads * (lq * (lk - lq) + lq * (lq + 1) // 2)
+                for lq, lk in zip(case.lens_q[:n], case.lens_k[:n]))
+    return dict(value=round(flops / t / 1e12, 5), unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"{name} prefill (index_copy_ store + SDPA per sequence, bottom-right causal mask"
+                       f"{', prefix pages gathered' if paged else ''}, bf16) over the first {n} of {S} sequences, "
+                       f"median of {reps}, {t:.3f} s each")
 
 
 def main(argv=None):
@@ -307,6 +366,7 @@ def main(argv=None):
     dev = torch.device("cuda:0")
     steps, warmup = args.steps, args.warmup
     out = {}
+    host = {}  # host copies of the cases for the CPU baselines
     if args.copy_probe:
         src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
@@ -323,10 +383,18 @@ def main(argv=None):
         log(f"[bench] cfg3 step {d3['step_ms']*1e3:.1f} us, attention {d3['attn_ms']*1e3:.1f} us "
             f"= {d3['attn_gbs']:.0f} GB/s, store {d3['store_ms']*1e3:.1f} us")
         out["cfg3"] = d3
-        # the CPU baseline runs last, so the GPU workloads follow each other
-        # without the GPU idling (and its clocks dropping) for the CPU sample
-        c3_host = None if args.no_cpu else c3.to("cpu")
+        # the CPU baselines run last, so the GPU workloads follow each other
+        # without the GPU idling (and its clocks dropping) for the CPU samples
+        if not args.no_cpu:
+            host["cfg3"] = c3.to("cpu")
         del c3
+        log("[bench] config 1: decode step, B=4 (cache-resident: no roofline claim)")
+        c1 = W.config1(dev)
+        out["cfg1"] = bench_decode(c1, steps, warmup, n_pools=1, warm_s=args.warm_seconds)
+        log(f"[bench] cfg1 step {out['cfg1']['step_ms']*1e3:.1f} us, attention {out['cfg1']['attn_ms']*1e3:.1f} us")
+        if not args.no_cpu:
+            host["cfg1"] = c1.to("cpu")
+        del c1
         torch.cuda.empty_cache()
     if args.only in (None, "prefill"):
         log("[bench] config 4: prefix-cached prefill (Qwen3-8B heads)")
@@ -336,6 +404,8 @@ def main(argv=None):
         out["store4"] = bench_store(c4, steps, warmup, args.warm_seconds)
         log(f"[bench] cfg4 store_kvcache {out['store4']['tokens']} tokens {out['store4']['ms']*1e3:.1f} us "
             f"= {out['store4']['gbs']:.0f} GB/s ({out['store4']['frac']:.3f} of 8 TB/s)")
+        if not args.no_cpu:
+            host["cfg4"] = W.config4("cpu")
         del c4
         log("[bench] config 2: varlen prefill")
         c2 = W.config2(dev)
@@ -344,6 +414,8 @@ def main(argv=None):
         out["store2"] = bench_store(c2, steps, warmup, args.warm_seconds)
         log(f"[bench] cfg2 store_kvcache {out['store2']['tokens']} tokens {out['store2']['ms']*1e3:.1f} us "
             f"= {out['store2']['gbs']:.0f} GB/s ({out['store2']['frac']:.3f} of 8 TB/s)")
+        if not args.no_cpu:
+            host["cfg2"] = W.config2("cpu")
         del c2
         torch.cuda.empty_cache()
     if args.only in (None, "producer"):
@@ -365,14 +437,25 @@ def main(argv=None):
         c5 = W.config5(dev)
         out["cfg5"] = bench_decode(c5, max(10, steps // 2), warmup, warm_s=args.warm_seconds)
         log(f"[bench] cfg5 attention {out['cfg5']['attn_ms']*1e3:.1f} us = {out['cfg5']['attn_gbs']:.0f} GB/s")
+        if not args.no_cpu:
+            host["cfg5"] = c5.to("cpu")
         del c5
         torch.cuda.empty_cache()
 
-    if args.only in (None, "decode") and not args.no_cpu:
-        log("[bench] CPU baseline (config 3 sample)")
-        out["cpu"] = cpu_baseline_decode(c3_host)
-        log(f"[bench] cpu {out['cpu']['value']:.2f} GB/s on {out['cpu']['cores']} threads")
-        del c3_host
+    if host:
+        torch.set_num_threads(os.cpu_count() or 1)
+        cpu = {}
+        budgets = {"cfg3": 16.0, "cfg1": 4.0, "cfg2": 8.0, "cfg4": 12.0, "cfg5": 12.0}
+        for name in ("cfg3", "cfg1", "cfg2", "cfg4", "cfg5"):
+            if name not in host:
+                continue
+            log(f"[bench] CPU baseline ({name} sample)")
+            case = host.pop(name)
+            fn = cpu_baseline_prefill if name in ("cfg2", "cfg4") else cpu_baseline_decode
+            cpu[name] = fn(case, name.replace("cfg", "config "), budgets[name])
+            log(f"[bench] cpu {name}: {cpu[name]['value']} {cpu[name]['unit']} on {cpu[name]['cores']} threads")
+            del case
+        out["cpu"] = cpu
 
     line = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
@@ -392,7 +475,14 @@ def main(argv=None):
                             "bytes_per_launch": d3["attn_bytes"], "launch_us": round(d3["attn_ms"] * 1e3, 2)}
         line["store_kvcache_us"] = round(d3["store_ms"] * 1e3, 2)
     if "cpu" in out:
-        line["cpu_baseline"] = out["cpu"]
+        if "cfg3" in out["cpu"]:
+            line["cpu_baseline"] = out["cpu"]["cfg3"]
+        line["cpu_baselines"] = out["cpu"]
+    if "cfg1" in out:
+        d1 = out["cfg1"]
+        line["cfg1_decode"] = {"note": "cache-resident (5 MB): reported, no roofline claim",
+                               "step_us": round(d1["step_ms"] * 1e3, 2), "attn_us": round(d1["attn_ms"] * 1e3, 2),
+                               "attn_gbs": round(d1["attn_gbs"], 1), "bytes": d1["attn_bytes"]}
     if "cfg4" in out or "cfg2" in out:
         line["prefill"] = {k: {"tflops": round(out[k]["tflops"], 1), "ms": round(out[k]["ms"], 4),
                                "gflop": round(out[k]["flops"] / 1e9, 2),
@@ -401,7 +491,9 @@ def main(argv=None):
     if "store4" in out or "store2" in out:
         line["store_kvcache_prefill"] = {
             k: {"tokens": out[s]["tokens"], "us": round(out[s]["ms"] * 1e3, 2), "bytes": out[s]["bytes"],
-                "gbs": round(out[s]["gbs"], 1), "frac": round(out[s]["frac"], 4)}
+                "gbs": round(out[s]["gbs"], 1), "frac": round(out[s]["frac"], 4),
+                "traffic": profiled_traffic(f"store_{k}", "store_hbm_traffic.md"),
+                "traffic_source": "profiles/store_hbm_traffic.md"}
             for k, s in (("cfg4", "store4"), ("cfg2", "store2")) if s in out}
     if "cfg5" in out:
         d5 = out["cfg5"]
