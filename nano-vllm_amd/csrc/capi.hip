@@ -191,7 +191,7 @@ int64_t nva_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num
                                    int32_t max_blocks_per_seq, int32_t block_size, int32_t kv_dtype,
                                    int32_t num_splits) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks_per_seq <= 0 || head_dim <= 0 ||
-      block_size <= 0 || num_splits < 0)
+      block_size <= 0 || num_splits < -1)
     return 0;
   const nva::DecodePlan plan =
       nva::plan_decode(batch, num_kv_heads, max_blocks_per_seq, block_size, kv_dtype, num_splits);
@@ -264,7 +264,7 @@ int decode_impl(const void* q, int64_t q_row_stride, const void* k_cache, const 
     return fail(NVA_ERR_UNSUPPORTED, "fp8 kv cache decode supports head_dim 128 only");
   if (batch < 0) return fail(NVA_ERR_INVALID_ARGUMENT, "batch must be >= 0");
   if (batch > 65535) return fail(NVA_ERR_UNSUPPORTED, "batch above 65535");
-  if (num_splits < 0) return fail(NVA_ERR_INVALID_ARGUMENT, "num_splits must be >= 0");
+  if (num_splits < -1) return fail(NVA_ERR_INVALID_ARGUMENT, "num_splits must be >= -1");
   if (block_size <= 0 || block_size % 32 != 0)
     return fail(NVA_ERR_UNSUPPORTED, "decode needs block_size a positive multiple of 32 (got %d)", block_size);
   if (max_blocks_per_seq <= 0 || bt_row_stride < max_blocks_per_seq)
@@ -336,6 +336,7 @@ int decode_impl(const void* q, int64_t q_row_stride, const void* k_cache, const 
   p.keys_per_split = plan.pages_per_split * block_size;
   p.num_splits = plan.num_splits;
   p.balanced_ranges = plan.balanced_ranges;
+  p.wg_split = plan.wg_split;
   p.head_dim = head_dim;
   p.scale_log2 = softmax_scale * kLog2e;
   return hip_status(nva::launch_decode(p, kv_dtype, static_cast<hipStream_t>(stream)), "decode launch");

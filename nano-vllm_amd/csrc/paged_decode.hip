@@ -228,12 +228,13 @@ __device__ __forceinline__ void compute_step(StepRegs<FP8>& r, int nvalid, int g
   }
 }
 
-// One wave, one kv head: attention of the head group's queries over keys
-// [k_begin, k_end) of sequence b.  Writes the normalised output when `direct`,
-// otherwise the unnormalised partial (O * v_scale, running max, sum) at `slot`.
+// One wave, one kv head: the unnormalised attention state of the head group's
+// queries over keys [k_begin, k_end) of sequence b -- O^T in acc (lane (n, g):
+// head n, columns 32g .. 32g+31), the running maximum m_run (log2 units) and
+// the row sum `l` (summed over the four lanes of a head).
 template <bool FP8, bool PREFETCH, int D>
-__device__ __forceinline__ void decode_segment(const DecodeParams& p, int kvh, int b, int k_begin, int k_end,
-                                               bool direct, int64_t slot) {
+__device__ __forceinline__ void segment_accumulate(const DecodeParams& p, int kvh, int b, int k_begin, int k_end,
+                                                   f32x4 (&acc)[8], float& m_run, float& l) {
   constexpr int EB = FP8 ? 1 : 2;  // bytes per cache element
   const int lane = threadIdx.x & 63;
   const int n = lane & 15;
@@ -266,10 +267,9 @@ __device__ __forceinline__ void decode_segment(const DecodeParams& p, int kvh, i
   }
   const float sl2 = FP8 ? p.scale_log2 * p.k_scale[kvh] : p.scale_log2;
 
-  f32x4 acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = kNegInf;
+  m_run = kNegInf;
   float l_run = 0.f;
 
   // Two register buffers: with PREFETCH the loads of step i+1 are in flight
@@ -293,9 +293,25 @@ __device__ __forceinline__ void decode_segment(const DecodeParams& p, int kvh, i
     }
   }
 
-  float l = l_run;
+  l = l_run;
   l += shfl_xor(l, 16);
   l += shfl_xor(l, 32);
+}
+
+// One wave, one kv head: attention of the head group's queries over keys
+// [k_begin, k_end) of sequence b.  Writes the normalised output when `direct`,
+// otherwise the unnormalised partial (O * v_scale, running max, sum) at `slot`.
+template <bool FP8, bool PREFETCH, int D>
+__device__ __forceinline__ void decode_segment(const DecodeParams& p, int kvh, int b, int k_begin, int k_end,
+                                               bool direct, int64_t slot) {
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const int h = kvh * p.group + n;
+  const bool head_ok = n < p.group;
+  f32x4 acc[8];
+  float m_run, l;
+  segment_accumulate<FP8, PREFETCH, D>(p, kvh, b, k_begin, k_end, acc, m_run, l);
   const float vscale = FP8 ? p.v_scale[kvh] : 1.0f;
   if (!head_ok || 32 * g >= D) return;  // lanes g >= D/32 hold no output columns
   if (direct) {
@@ -353,6 +369,73 @@ __global__ __launch_bounds__(64 * WAVES) void paged_decode_split_kernel(DecodePa
   if (k_begin >= k_end && !direct) return;  // the merge reads only splits that hold keys
   decode_segment<FP8, PREFETCH, D>(p, kvh, b, k_begin, max(k_begin, k_end), direct,
                                    static_cast<int64_t>(b) * p.num_splits + split);
+}
+
+// ---------------------------------------------------------------------------
+// Workgroup split-K for small batches: workgroup = (kv head, sequence), its
+// kWgWaves waves take consecutive equal shares of the sequence's 32-key steps
+// and merge their partial states in LDS (log-sum-exp, as decode_merge_kernel),
+// so nothing goes through global memory and no merge launch follows.  Used when
+// batch * num_kv_heads workgroups leave the GPU under-filled anyway and every
+// wave's share is short (plan_decode), where the balanced mode's extra launch
+// and partial round trip dominate (a captured small-batch step is three short
+// launches per layer otherwise).  Grid: (num_kv_heads, batch).
+// ---------------------------------------------------------------------------
+template <bool FP8, int D>
+__global__ __launch_bounds__(64 * kWgWaves) void paged_decode_wgsplit_kernel(DecodeParams p) {
+  __shared__ f32x4 s_acc[kWgWaves][8][64];  // O^T partial of lane l, register j, wave w
+  __shared__ float s_m[kWgWaves][64];
+  __shared__ float s_l[kWgWaves][64];
+  const int kvh = blockIdx.x;
+  const int b = blockIdx.y;
+  const int w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int ctx = clamped_len(p, b);
+  const int steps = (ctx + 31) >> 5;
+  const int per = (steps + kWgWaves - 1) / kWgWaves;
+  const int k_begin = min(ctx, 32 * per * w);
+  const int k_end = min(ctx, 32 * per * (w + 1));
+  f32x4 acc[8];
+  float m_run, l;
+  segment_accumulate<FP8, false, D>(p, kvh, b, k_begin, k_end, acc, m_run, l);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s_acc[w][j][lane] = acc[j];
+  s_m[w][lane] = m_run;
+  s_l[w][lane] = l;
+  __syncthreads();
+  if (w != 0) return;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const int h = kvh * p.group + n;
+  if (n >= p.group || 32 * g >= D) return;  // lanes with no head or no output columns
+  float M = kNegInf;
+#pragma unroll
+  for (int i = 0; i < kWgWaves; ++i) M = fmaxf(M, s_m[i][lane]);
+  float L = 0.f;
+  f32x4 o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (M != kNegInf) {
+#pragma unroll
+    for (int i = 0; i < kWgWaves; ++i) {
+      const float mi = s_m[i][lane];
+      if (mi == kNegInf) continue;  // a wave with no key of this sequence
+      const float c = fast_exp2(mi - M);
+      L += c * s_l[i][lane];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] += c * s_acc[i][j][lane];
+    }
+  }
+  const float vscale = FP8 ? p.v_scale[kvh] : 1.0f;
+  const float inv = L > 0.f ? vscale / L : 0.f;
+  uint16_t* orow = p.out + b * p.out_row_stride + h * D + 32 * g;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    u32x4 v;
+#pragma unroll
+    for (int q2 = 0; q2 < 4; ++q2) v[q2] = pack_bf16x2(o[2 * q2][r] * inv, o[2 * q2 + 1][r] * inv);
+    st16(orow + 8 * r, v);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -581,6 +664,18 @@ int decode_waves_per_group(int32_t num_kv_heads, int32_t kv_dtype) {
 DecodePlan plan_decode(int32_t batch, int32_t num_kv_heads, int32_t max_blocks, int32_t block_size,
                        int32_t kv_dtype, int32_t requested_splits) {
   DecodePlan plan{};
+  // small batch, short table: the workgroup split (no workspace, no merge launch)
+  const int64_t table_keys = static_cast<int64_t>(max_blocks) * block_size;
+  if (requested_splits == 0 && static_cast<int64_t>(batch) * num_kv_heads <= kWgMaxGroups &&
+      table_keys <= int64_t{32} * kWgMaxStepsPerWave * kWgWaves) {
+    plan.pages_per_split = max_blocks;
+    plan.num_splits = 1;
+    plan.balanced_ranges = 0;
+    plan.wg_split = 1;
+    plan.partial_slots = 0;
+    return plan;
+  }
+  if (requested_splits < 0) requested_splits = 0;  // -1: balanced whatever the sizes
   if (requested_splits > 0) {  // fixed: about requested_splits splits per sequence
     int32_t pps = (max_blocks + requested_splits - 1) / requested_splits;
     if (pps < 1) pps = 1;
@@ -622,7 +717,11 @@ static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
   else                                                                                                  \
     hipLaunchKernelGGL((KERNEL<FP8, 1, PF, D>), GRID, dim3(64), 0, stream, p);
   bool merge;
-  if (p.balanced_ranges > 0) {
+  if (p.wg_split) {
+    const dim3 grid(static_cast<unsigned>(p.num_kv_heads), static_cast<unsigned>(p.batch));
+    hipLaunchKernelGGL((paged_decode_wgsplit_kernel<FP8, D>), grid, dim3(64 * kWgWaves), 0, stream, p);
+    merge = false;
+  } else if (p.balanced_ranges > 0) {
     const dim3 grid(static_cast<unsigned>(p.balanced_ranges), groups);
     NVA_LAUNCH_W(paged_decode_balanced_kernel, grid);
     merge = true;

@@ -214,7 +214,8 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     """Paged decode, one query per sequence (attention.py:75-77).
     q (B, 1, nh, d) -> (B, 1, nh, d).  `causal` is accepted for signature parity
     and is a no-op for a single query; num_splits has flash-attn's meaning
-    (0 = heuristic)."""
+    (0 = heuristic, n > 0 = about n splits per sequence), and -1 selects the
+    balanced split-K whatever the sizes."""
     del causal
     if q.dim() != 4 or q.shape[1] != 1:
         raise RuntimeError("q must be (batch, 1, num_heads, head_dim)")

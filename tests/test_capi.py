@@ -140,7 +140,7 @@ def decode(lib, **kw):
     (dict(num_blocks=0), _capi.NVA_ERR_INVALID_ARGUMENT),
     (dict(q=None), _capi.NVA_ERR_INVALID_ARGUMENT),
     (dict(out=C + 8), _capi.NVA_ERR_UNSUPPORTED),
-    (dict(num_splits=-1), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(num_splits=-2), _capi.NVA_ERR_INVALID_ARGUMENT),
     (dict(scale=-1.0), _capi.NVA_ERR_INVALID_ARGUMENT),
     (dict(), _capi.NVA_ERR_WORKSPACE),                               # split-K needs a workspace
     (dict(workspace=A, workspace_bytes=16), _capi.NVA_ERR_WORKSPACE),
@@ -162,8 +162,15 @@ def test_decode_workspace_plan(lib):
     assert f(256, 16, 8, 128, 8, 256, 0, 0) == rnd((256 + 128) * 16 * 130 * 4 + 257 * 4)
     # fp8: ranges of 8 kv-head waves, about 2048 waves
     assert f(64, 64, 8, 128, 128, 256, 1, 0) == rnd((64 + 256) * 64 * 130 * 4 + 65 * 4)
-    # never more ranges than steps: 2 sequences x 1 page x 8 steps
-    assert f(2, 16, 8, 128, 1, 256, 0, 0) == rnd((2 + 16) * 16 * 130 * 4 + 3 * 4)
+    # never more ranges than steps: 2 sequences x 1 page x 8 steps (balanced forced with -1)
+    assert f(2, 16, 8, 128, 1, 256, 0, -1) == rnd((2 + 16) * 16 * 130 * 4 + 3 * 4)
+    # small batch, short table (batch * nkv <= 256, table <= 8 waves x 16 steps x 32 keys):
+    # the workgroup split, which merges in LDS and needs no workspace
+    assert f(2, 16, 8, 128, 1, 256, 0, 0) == 0
+    assert f(32, 16, 8, 128, 16, 256, 0, 0) == 0
+    assert f(32, 16, 8, 128, 16, 256, 1, 0) == 0
+    assert f(33, 16, 8, 128, 16, 256, 0, 0) > 0   # 264 workgroups: balanced
+    assert f(4, 16, 8, 128, 17, 256, 0, 0) > 0    # 4352-key table: balanced
     # deterministic, and nothing for an empty batch
     assert f(64, 64, 8, 128, 128, 256, 1, 0) == f(64, 64, 8, 128, 128, 256, 1, 0) > 0
     assert f(0, 16, 8, 128, 8, 256, 0, 0) == 0

@@ -138,7 +138,7 @@ def _run_decode(case, num_splits=0, store=True):
     return f32(o[:, 0])
 
 
-@pytest.mark.parametrize("num_splits", [0, 1, 2, 3])
+@pytest.mark.parametrize("num_splits", [0, -1, 1, 2, 3])
 def test_decode_cfg1(dev, num_splits):
     from nanovllm_amd import workloads as W
     case = W.config1("cpu").to(dev)
@@ -197,19 +197,51 @@ def test_decode_group_sizes(dev, nh, nkv, fp8):
 ])
 @pytest.mark.parametrize("fp8", [False, True])
 def test_decode_balanced_partition(dev, lengths, width, fp8):
-    """Balanced split-K (num_splits=0) against the oracle and against fixed splits."""
+    """Balanced split-K (num_splits=-1 forces it at these small batches) against the
+    oracle and against fixed splits and the size heuristic (0)."""
     from nanovllm_amd import workloads as W
     case = W.make_decode_case(len(lengths), 32, 8, 0, 0, 64, fp8=fp8, seed=len(lengths) + width,
                               bulk_device=dev, lengths=lengths, table_width=width)
-    bal = _run_decode(case, 0, store=False)
+    bal = _run_decode(case, -1, store=False)
     tol = dict(max_abs=FP8_MAX_ABS, mean_abs=FP8_MAX_ABS) if fp8 else {}
     assert_attn_close(bal, decode_reference(case), what=f"balanced {lengths}", **tol)
-    for ns in (1, 3):
+    for ns in (0, 1, 3):
         fixed = _run_decode(case, ns, store=False)
         assert np.abs(fixed - bal).max() <= 1e-2
     for b, L in enumerate(lengths):
         if L == 0:
             assert np.all(bal[b] == 0)
+
+
+@pytest.mark.parametrize("nh,nkv,d", [(16, 8, 128), (32, 8, 128), (128, 8, 128), (8, 1, 128), (14, 2, 64),
+                                      (16, 8, 64)])
+@pytest.mark.parametrize("fp8", [False, True])
+def test_decode_workgroup_split(dev, nh, nkv, d, fp8):
+    """The small-batch workgroup split (8 waves share a sequence's steps and merge
+    in LDS): ragged lengths incl. 0, 1 and a full 16-page table, at batches of 1 to
+    the largest it serves (batch * nkv = 256), against the oracle and the balanced
+    mode."""
+    if fp8 and d != 128:
+        pytest.skip("fp8 decode supports head_dim 128 only (nva_decode refuses it)")
+    from nanovllm_amd import workloads as W
+    from nanovllm_amd import _capi
+    for B in (1, 3, 256 // nkv):
+        g = torch.Generator().manual_seed(B + nh)
+        lengths = torch.randint(0, 4097, (B,), generator=g).tolist()
+        lengths[0] = 4096 if B > 1 else 700
+        if B > 2:
+            lengths[1], lengths[2] = 0, 1
+        case = W.make_decode_case(B, nh, nkv, 0, 0, 16 * B + 1, fp8=fp8, seed=B * 7 + nh, head_dim=d,
+                                  bulk_device=dev, lengths=lengths, table_width=16)
+        assert _capi.load().nva_decode_workspace_bytes(B, nh, nkv, d, 16, 256, int(fp8), 0) == 0
+        got = _run_decode(case, 0, store=False)
+        tol = dict(max_abs=FP8_MAX_ABS, mean_abs=FP8_MAX_ABS) if fp8 else {}
+        assert_attn_close(got, decode_reference(case), what=f"wg split B={B} nh={nh} nkv={nkv} d={d}", **tol)
+        bal = _run_decode(case, -1, store=False)
+        assert np.abs(got - bal).max() <= 1e-2
+        for b, L in enumerate(lengths):
+            if L == 0:
+                assert np.all(got[b] == 0)
 
 
 def test_decode_balanced_many_sequences(dev):
