@@ -47,7 +47,7 @@ class DecodeCase:
 
     @property
     def batch(self) -> int:
-        return self.q.shape[0]
+        return self.context_lens.shape[0]
 
     def kv_bytes(self) -> int:
         """Algorithmic HBM bytes of one decode: every visible K and V element once,
