@@ -202,17 +202,19 @@ struct ItemDesc {
   bool valid;  // false: no item (s < 0) or a tile past the sequence's end
 };
 
-__device__ __forceinline__ ItemDesc item_desc(const PrefillParams& p, int s, int kvh, int tile) {
+// cu_q / cu_k: cu_seqlens_q / cu_seqlens_k, in global memory or a copy in LDS.
+__device__ __forceinline__ ItemDesc item_desc(const PrefillParams& p, const int* cu_q, const int* cu_k, int s, int kvh,
+                                              int tile) {
   ItemDesc d{};
   d.s = s;
   d.kvh = kvh;
   d.tile = tile;
   d.valid = false;
   if (s < 0) return d;
-  d.q_start = p.cu_q[s];
-  d.Lq = p.cu_q[s + 1] - d.q_start;
-  d.k_start = p.cu_k[s];
-  d.Lk = p.cu_k[s + 1] - d.k_start;
+  d.q_start = __builtin_amdgcn_readfirstlane(cu_q[s]);
+  d.Lq = __builtin_amdgcn_readfirstlane(cu_q[s + 1]) - d.q_start;
+  d.k_start = __builtin_amdgcn_readfirstlane(cu_k[s]);
+  d.Lk = __builtin_amdgcn_readfirstlane(cu_k[s + 1]) - d.k_start;
   d.i0 = tile * p.positions_per_tile;
   d.valid = d.i0 < d.Lq;
   const int last_pos = min(d.i0 + p.positions_per_tile, d.Lq) - 1;
@@ -615,7 +617,7 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   const int s = blockIdx.x / p.num_kv_heads;
   const int kvh = blockIdx.x - s * p.num_kv_heads;
   const int tile = p.num_q_tiles - 1 - static_cast<int>(blockIdx.y);
-  const ItemDesc it = item_desc(p, s, kvh, tile);
+  const ItemDesc it = item_desc(p, p.cu_q, p.cu_k, s, kvh, tile);
   if (!it.valid) return;
   bf16x8 qop[D / 16];
   item_fetch_q<D>(p, it, qop);
@@ -632,8 +634,10 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
 // tiles past the shorter sequences' ends; they exit at once, but a workgroup
 // dispatcher that waits for a particular busy CU then leaves other CUs idle
 // for a whole workgroup's duration (measured: half the CUs idle for the first
-// ~40 us of config 4).  Here every workgroup builds the same table of real
-// items from cu_seqlens_q -- item order: query tile index descending (the
+// ~40 us of config 4).  Here every workgroup copies cu_seqlens_q/k into LDS
+// (so locating an item needs no global load, whose scalar-cache wait would
+// also hold up the LDS waits around it) and builds the same table of real
+// items from them -- item order: query tile index descending (the
 // heavier tiles first), then sequence, then kv head -- and takes items
 // g, then 2 NW - 1 - g, ... (a snake over the NW workgroups, which balances
 // their totals).  Workgroup g = 8 m + x runs on XCD x, and the snake reverses
@@ -678,6 +682,7 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(
   __shared__ __attribute__((aligned(1024))) char smem_all[kStages * Geom<D>::kStageBytes];
   __shared__ int s_ntq[kPersistMaxSeqs];           // query tiles of each sequence
   __shared__ int s_start[kPersistMaxTiles + 1];    // first item of each tile level (level T_max: total)
+  __shared__ int s_cu[2][kPersistMaxSeqs + 1];     // cu_seqlens_q and cu_seqlens_k
   __shared__ uint32_t s_claim;                     // the queue claim, broadcast by thread 0
   const int tid = threadIdx.x;
   const int S = p.num_seqs;
@@ -688,9 +693,13 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(
   // level table: cnt[t] = #{s : ntq_s > t}; items of level t (query tile t of
   // those sequences, all kv heads) start at s_start[t] = nkv * sum_{t' > t} cnt[t']
   for (int i = tid; i <= T; i += kThreads) s_start[i] = 0;
+  for (int i = tid; i <= S; i += kThreads) {
+    s_cu[0][i] = p.cu_q[i];
+    s_cu[1][i] = p.cu_k[i];
+  }
   __syncthreads();
   for (int i = tid; i < S; i += kThreads) {
-    const int lq = p.cu_q[i + 1] - p.cu_q[i];
+    const int lq = s_cu[0][i + 1] - s_cu[0][i];
     const int nt = lq > 0 ? min((lq + BP - 1) / BP, T) : 0;
     s_ntq[i] = nt;
     if (nt > 0) atomicAdd(&s_start[nt - 1], 1);  // histogram of ntq (bin nt - 1)
@@ -739,7 +748,7 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(
   // Table item `item` (every item below `total` is a real tile: its sequence
   // has more than t query tiles), or an invalid descriptor past the end.
   auto desc_of = [&](int item) {
-    if (item >= total) return item_desc(p, -1, 0, 0);
+    if (item >= total) return item_desc(p, s_cu[0], s_cu[1], -1, 0, 0);
     // level t: the smallest t with start[t] <= item (start decreases in t)
     int lo = 0, hi = T - 1;
     while (lo < hi) {
@@ -751,7 +760,7 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(
     const int j = item - __builtin_amdgcn_readfirstlane(s_start[t]);
     const int rank = j / nkv;
     const int kvh = j - rank * nkv;
-    return item_desc(p, find_seq(s_ntq, S, t, rank), kvh, t);
+    return item_desc(p, s_cu[0], s_cu[1], find_seq(s_ntq, S, t, rank), kvh, t);
   };
   // QUEUE: the launch guarantees NW % 8 == 0, so lane x is the XCD
   constexpr int L = kPrefillQueueLanes;
@@ -774,7 +783,7 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(
   item_fetch_q<D>(p, cur, qop);
   item_fetch_tiles<PAGED, D>(p, smem_all, cur);
   for (int round = 1;; ++round) {
-    // the next item is located (and its cu_seqlens read) while this one's
+    // the next item is located (from the LDS tables) while this one's
     // first copies are in flight; its own first copies start in this one's
     // epilogue
     ItemDesc nxt;
