@@ -336,7 +336,7 @@ int decode_impl(const void* q, int64_t q_row_stride, const void* k_cache, const 
   p.keys_per_split = plan.pages_per_split * block_size;
   p.num_splits = plan.num_splits;
   p.balanced_ranges = plan.balanced_ranges;
-  p.wg_split = plan.wg_split;
+  p.spread = plan.spread;
   p.head_dim = head_dim;
   p.scale_log2 = softmax_scale * kLog2e;
   return hip_status(nva::launch_decode(p, kv_dtype, static_cast<hipStream_t>(stream)), "decode launch");

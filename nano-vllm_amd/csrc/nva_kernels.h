@@ -49,7 +49,7 @@ struct DecodeParams {
   int32_t keys_per_split;     // fixed mode: multiple of block_size
   int32_t num_splits;         // fixed mode: splits per sequence
   int32_t balanced_ranges;    // balanced mode: number of step ranges P (0 = fixed mode)
-  int32_t wg_split;           // 1: workgroup split-K with an LDS merge (small batches)
+  int32_t spread;             // > 0: spread mode with that many shares per sequence (small batches)
   int32_t head_dim;           // 64 or 128
   float scale_log2;           // softmax_scale * log2(e)
 };
@@ -141,15 +141,16 @@ struct DecodePlan {
   int32_t pages_per_split;
   int32_t num_splits;
   int32_t balanced_ranges;
-  int32_t wg_split;           // 1: workgroup split-K (no workspace)
+  int32_t spread;             // > 0: spread mode, shares per sequence
   int64_t partial_slots;      // partial (O, max, sum) slots the workspace holds
 };
-// Workgroup split-K (small batches): waves per workgroup, the largest
-// batch * num_kv_heads it serves, and the most 32-key steps per wave the block
-// table's width may imply.
-constexpr int kWgWaves = 8;
-constexpr int kWgMaxGroups = 256;
-constexpr int kWgMaxStepsPerWave = 16;
+// Spread mode (small batches): the largest batch * num_kv_heads it serves, the
+// waves it aims for in total, and the widest block table (one wave holds a row,
+// one entry per lane).
+constexpr int kSpreadMaxPairs = 256;
+constexpr int kSpreadTargetWaves = 1024;
+constexpr int kWgMaxBlocks = 64;
+
 DecodePlan plan_decode(int32_t batch, int32_t num_kv_heads, int32_t max_blocks,
                        int32_t block_size, int32_t kv_dtype, int32_t requested_splits);
 

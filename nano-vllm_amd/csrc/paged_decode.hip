@@ -121,11 +121,13 @@ struct WaveItem {
 
 // Slot of the first key of step i and how many of its 32 keys exist (0 when the
 // block id is outside the pool: those keys stay masked and nothing is read from
-// the bad page).
-__device__ __forceinline__ int64_t step_row(const WaveItem& w, int i, int& nvalid) {
+// the bad page).  HOIST: lane j of bt_row holds block-table entry j (the whole
+// row, read before the loop), so the step needs no dependent load.
+template <bool HOIST = false>
+__device__ __forceinline__ int64_t step_row(const WaveItem& w, int i, int& nvalid, int bt_row = 0) {
   const int key0 = w.k_begin + 32 * i;
   const int blk = key0 / w.block_size;
-  const int page = w.bt[blk];
+  const int page = HOIST ? __builtin_amdgcn_readlane(bt_row, blk) : w.bt[blk];
   const bool ok = page >= 0 && page < w.num_blocks;
   nvalid = ok ? min(32, w.k_end - key0) : 0;
   return static_cast<int64_t>(ok ? page : 0) * w.block_size + (key0 - blk * w.block_size);
@@ -157,11 +159,72 @@ __device__ __forceinline__ void load_step(StepRegs<FP8>& r, const WaveItem& w, i
   }
 }
 
-// Online-softmax update of one step: scores, running max/sum, O^T += V^T P^T.
+// A step as two buffer resources (its 32 K rows and 32 V rows of this kv head)
+// and its count of keys.  Rows past the last valid key, every row of a block
+// id outside the pool and every row of a step past the segment's end lie
+// outside the resource's records: their loads return zeros without touching
+// memory.  Loads can thus be issued for steps that do not exist, so every
+// path issues the same loads and the compiler's wait before a step's compute
+// covers only that step's loads (a prefetch issued on one path only makes it
+// wait for everything in flight).
+struct StepRsrc {
+  __amdgpu_buffer_rsrc_t k, v;
+  int nvalid;
+};
+
+// Records covering rows [0, nvalid) of a step whose row 0 is at `base`.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const char* base, int nvalid, int slot_bytes, int row_bytes) {
+  const int records = nvalid > 0 ? (nvalid - 1) * slot_bytes + row_bytes : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0, records, 0x00020000);
+}
+
+template <bool HOIST, int ROW_BYTES>
+__device__ __forceinline__ StepRsrc step_rsrc(const WaveItem& w, int i, int nsteps, int bt_row) {
+  StepRsrc r;
+  int nvalid = 0;
+  int64_t row0 = 0;
+  if (i < nsteps) row0 = step_row<HOIST>(w, i, nvalid, bt_row);
+  const int sb = static_cast<int>(w.slot_bytes);
+  r.k = rows_rsrc(w.kbase + row0 * w.slot_bytes, nvalid, sb, ROW_BYTES);
+  r.v = rows_rsrc(w.vbase + row0 * w.slot_bytes, nvalid, sb, ROW_BYTES);
+  r.nvalid = nvalid;
+  return r;
+}
+
+// load_step through the step's buffer resources; lanes with no value columns
+// (D = 64) read at an offset past every record.
 template <bool FP8, int D>
+__device__ __forceinline__ void load_step_buf(StepRegs<FP8>& r, const WaveItem& w, const StepRsrc& rs) {
+  const int sb = static_cast<int>(w.slot_bytes);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int ro = (w.krow0 + 4 * t) * sb;
+    if constexpr (!FP8) {
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s)
+        r.k[t][s] = __builtin_amdgcn_raw_buffer_load_b128(rs.k, ro + qk_dim<false>(s, w.g) * 2, 0, 0);
+    } else {
+#pragma unroll
+      for (int u = 0; u < D / 64; ++u) r.k[t][u] = __builtin_amdgcn_raw_buffer_load_b128(rs.k, ro + 64 * u + 16 * w.g, 0, 0);
+    }
+  }
+  const bool has_cols = D == 128 || w.n < D / 8;
+  const int col = has_cols ? (FP8 ? 8 : 16) * w.n : 0x7fffffff - 32 * sb;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int off = (8 * w.g + i) * sb + col;
+    if constexpr (!FP8)
+      r.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs.v, off, 0, 0);
+    else
+      r.v[i] = __builtin_amdgcn_raw_buffer_load_b64(rs.v, off, 0, 0);
+  }
+}
+
+// Online-softmax update of one step: scores, running max/sum, O^T += V^T P^T.
+template <bool FP8, int D, bool ZERO_ROWS = true>
 __device__ __forceinline__ void compute_step(StepRegs<FP8>& r, int nvalid, int g, const bf16x8 (&qop)[4],
                                              float sl2, f32x4 (&acc)[8], float& m_run, float& l_run) {
-  if (nvalid < 32) {  // keys past the end (or on a bad page) contribute nothing
+  if (ZERO_ROWS && nvalid < 32) {  // keys past the end (or on a bad page) contribute nothing
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       if (8 * g + i >= nvalid) {
@@ -232,9 +295,9 @@ __device__ __forceinline__ void compute_step(StepRegs<FP8>& r, int nvalid, int g
 // queries over keys [k_begin, k_end) of sequence b -- O^T in acc (lane (n, g):
 // head n, columns 32g .. 32g+31), the running maximum m_run (log2 units) and
 // the row sum `l` (summed over the four lanes of a head).
-template <bool FP8, bool PREFETCH, int D>
+template <bool FP8, bool PREFETCH, int D, bool HOIST = false, bool BUF = false>
 __device__ __forceinline__ void segment_accumulate(const DecodeParams& p, int kvh, int b, int k_begin, int k_end,
-                                                   f32x4 (&acc)[8], float& m_run, float& l) {
+                                                   f32x4 (&acc)[8], float& m_run, float& l, int bt_row = 0) {
   constexpr int EB = FP8 ? 1 : 2;  // bytes per cache element
   const int lane = threadIdx.x & 63;
   const int n = lane & 15;
@@ -275,21 +338,36 @@ __device__ __forceinline__ void segment_accumulate(const DecodeParams& p, int kv
   // Two register buffers: with PREFETCH the loads of step i+1 are in flight
   // while step i is computed.
   const int nsteps = (k_end - k_begin + 31) >> 5;
-  if (nsteps > 0) {
+  if (BUF && nsteps > 0) {
+    // two steps in flight: step i+1's loads go out before step i is computed,
+    // step i+2's before step i+1 (past the end they return zeros)
+    constexpr int RB = D * EB;
+    StepRegs<FP8> A, B;
+    StepRsrc ra = step_rsrc<HOIST, RB>(w, 0, nsteps, bt_row);
+    load_step_buf<FP8, D>(A, w, ra);
+    for (int i = 0; i < nsteps; i += 2) {
+      const StepRsrc rb = step_rsrc<HOIST, RB>(w, i + 1, nsteps, bt_row);
+      load_step_buf<FP8, D>(B, w, rb);
+      compute_step<FP8, D, false>(A, ra.nvalid, g, qop, sl2, acc, m_run, l_run);
+      ra = step_rsrc<HOIST, RB>(w, i + 2, nsteps, bt_row);
+      load_step_buf<FP8, D>(A, w, ra);
+      if (i + 1 < nsteps) compute_step<FP8, D, false>(B, rb.nvalid, g, qop, sl2, acc, m_run, l_run);
+    }
+  } else if (nsteps > 0) {
     StepRegs<FP8> A, B;
     int nvA = 0, nvB = 0;
-    load_step<FP8, D>(A, w, step_row(w, 0, nvA));
+    load_step<FP8, D>(A, w, step_row<HOIST>(w, 0, nvA, bt_row));
     for (int i = 0; i < nsteps; i += 2) {
       const bool has1 = i + 1 < nsteps;
       const bool has2 = i + 2 < nsteps;
-      if (PREFETCH && has1) load_step<FP8, D>(B, w, step_row(w, i + 1, nvB));
+      if (PREFETCH && has1) load_step<FP8, D>(B, w, step_row<HOIST>(w, i + 1, nvB, bt_row));
       compute_step<FP8, D>(A, nvA, g, qop, sl2, acc, m_run, l_run);
       if (has1) {
-        if (!PREFETCH) load_step<FP8, D>(B, w, step_row(w, i + 1, nvB));
-        if (PREFETCH && has2) load_step<FP8, D>(A, w, step_row(w, i + 2, nvA));
+        if (!PREFETCH) load_step<FP8, D>(B, w, step_row<HOIST>(w, i + 1, nvB, bt_row));
+        if (PREFETCH && has2) load_step<FP8, D>(A, w, step_row<HOIST>(w, i + 2, nvA, bt_row));
         compute_step<FP8, D>(B, nvB, g, qop, sl2, acc, m_run, l_run);
       }
-      if (!PREFETCH && has2) load_step<FP8, D>(A, w, step_row(w, i + 2, nvA));
+      if (!PREFETCH && has2) load_step<FP8, D>(A, w, step_row<HOIST>(w, i + 2, nvA, bt_row));
     }
   }
 
@@ -372,70 +450,79 @@ __global__ __launch_bounds__(64 * WAVES) void paged_decode_split_kernel(DecodePa
 }
 
 // ---------------------------------------------------------------------------
-// Workgroup split-K for small batches: workgroup = (kv head, sequence), its
-// kWgWaves waves take consecutive equal shares of the sequence's 32-key steps
-// and merge their partial states in LDS (log-sum-exp, as decode_merge_kernel),
-// so nothing goes through global memory and no merge launch follows.  Used when
-// batch * num_kv_heads workgroups leave the GPU under-filled anyway and every
-// wave's share is short (plan_decode), where the balanced mode's extra launch
-// and partial round trip dominate (a captured small-batch step is three short
-// launches per layer otherwise).  Grid: (num_kv_heads, batch).
+// Spread split-K for small batches: one wave per workgroup; workgroup
+// (r, kvh, b) takes the r-th share of sequence b's 32-key steps.  One CU moves
+// a step's 16 KiB slowly (about 16 bytes per cycle with eight waves loading,
+// measured), so a small batch is spread over many CUs: S shares per
+// (sequence, kv head), S = kSpreadTargetWaves / (batch * num_kv_heads) capped
+// by the table's steps (plan_decode).  Shares are ceil(steps / S) steps; the
+// S_b = ceil(steps / share) non-empty ones each write their partial
+// (O * v_scale, max, sum) to slot b * S + r for decode_spread_merge_kernel.  A
+// sequence with one share (or none: zeros) is written directly.  (Merging in
+// this launch instead -- the last share to arrive on a device counter merges --
+// measured slower: arrivals on one counter serialise at ~500 cycles each, and
+// the release/acquire fences cost as much again.)  Grid: (S, num_kv_heads, batch).
 // ---------------------------------------------------------------------------
+// Steps per share and the number of non-empty shares of a sequence of `steps`
+// steps cut into at most S shares.
+__device__ __forceinline__ void spread_shares(int steps, int S, int& per, int& shares) {
+  per = steps > 0 ? (steps + S - 1) / S : 1;
+  shares = (steps + per - 1) / per;
+}
+
 template <bool FP8, int D>
-__global__ __launch_bounds__(64 * kWgWaves) void paged_decode_wgsplit_kernel(DecodeParams p) {
-  __shared__ f32x4 s_acc[kWgWaves][8][64];  // O^T partial of lane l, register j, wave w
-  __shared__ float s_m[kWgWaves][64];
-  __shared__ float s_l[kWgWaves][64];
-  const int kvh = blockIdx.x;
-  const int b = blockIdx.y;
-  const int w = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int ctx = clamped_len(p, b);
-  const int steps = (ctx + 31) >> 5;
-  const int per = (steps + kWgWaves - 1) / kWgWaves;
-  const int k_begin = min(ctx, 32 * per * w);
-  const int k_end = min(ctx, 32 * per * (w + 1));
+__global__ __launch_bounds__(64) void paged_decode_spread_kernel(DecodeParams p) {
+  const int r = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int S = p.spread;
+  const int lane = threadIdx.x;
+  // the whole block-table row (at most kWgMaxBlocks entries), read together
+  // with the context length instead of one dependent read per step
+  const int bt_row = lane < p.max_blocks ? p.block_table[b * p.bt_row_stride + lane] : -1;
+  const int ctx = __builtin_amdgcn_readfirstlane(clamped_len(p, b));
+  int per, shares;  // shares: the non-empty ones (0 for an empty sequence)
+  spread_shares((ctx + 31) >> 5, S, per, shares);
+  const bool direct = shares <= 1;
+  if (r >= (direct ? 1 : shares)) return;
+  const int k_begin = min(ctx, 32 * per * r);
+  const int k_end = min(ctx, 32 * per * (r + 1));
   f32x4 acc[8];
   float m_run, l;
-  segment_accumulate<FP8, false, D>(p, kvh, b, k_begin, k_end, acc, m_run, l);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) s_acc[w][j][lane] = acc[j];
-  s_m[w][lane] = m_run;
-  s_l[w][lane] = l;
-  __syncthreads();
-  if (w != 0) return;
+  segment_accumulate<FP8, true, D, true, true>(p, kvh, b, k_begin, k_end, acc, m_run, l, bt_row);
   const int n = lane & 15;
   const int g = lane >> 4;
+  const bool cols = n < p.group && 32 * g < D;  // lanes holding a head's output columns
   const int h = kvh * p.group + n;
-  if (n >= p.group || 32 * g >= D) return;  // lanes with no head or no output columns
-  float M = kNegInf;
-#pragma unroll
-  for (int i = 0; i < kWgWaves; ++i) M = fmaxf(M, s_m[i][lane]);
-  float L = 0.f;
-  f32x4 o[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (M != kNegInf) {
-#pragma unroll
-    for (int i = 0; i < kWgWaves; ++i) {
-      const float mi = s_m[i][lane];
-      if (mi == kNegInf) continue;  // a wave with no key of this sequence
-      const float c = fast_exp2(mi - M);
-      L += c * s_l[i][lane];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] += c * s_acc[i][j][lane];
-    }
-  }
   const float vscale = FP8 ? p.v_scale[kvh] : 1.0f;
-  const float inv = L > 0.f ? vscale / L : 0.f;
-  uint16_t* orow = p.out + b * p.out_row_stride + h * D + 32 * g;
+  if (direct) {
+    if (!cols) return;
+    const float inv = l > 0.f ? vscale / l : 0.f;
+    uint16_t* orow = p.out + b * p.out_row_stride + h * D + 32 * g;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    u32x4 v;
+    for (int q = 0; q < 4; ++q) {
+      u32x4 o;
 #pragma unroll
-    for (int q2 = 0; q2 < 4; ++q2) v[q2] = pack_bf16x2(o[2 * q2][r] * inv, o[2 * q2 + 1][r] * inv);
-    st16(orow + 8 * r, v);
+      for (int q2 = 0; q2 < 4; ++q2) o[q2] = pack_bf16x2(acc[2 * q2][q] * inv, acc[2 * q2 + 1][q] * inv);
+      st16(orow + 8 * q, o);
+    }
+    return;
   }
+  if (!cols) return;
+  const int64_t idx = (static_cast<int64_t>(b) * S + r) * p.num_heads + h;
+  float* wo = p.ws_o + idx * D + 32 * g;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    f32x4 lo, hi;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lo[j] = acc[j][q] * vscale;
+      hi[j] = acc[4 + j][q] * vscale;
+    }
+    *reinterpret_cast<f32x4*>(wo + 8 * q) = lo;
+    *reinterpret_cast<f32x4*>(wo + 8 * q + 4) = hi;
+  }
+  if (g == 0) *reinterpret_cast<f32x2*>(p.ws_ml + idx * 2) = f32x2{m_run, l};
 }
 
 // ---------------------------------------------------------------------------
@@ -631,6 +718,70 @@ __global__ __launch_bounds__(64 * kMergeHeads) void decode_merge_kernel(DecodePa
   *orow = pack_bf16x2(o0 * inv, o1 * inv);
 }
 
+// Merge of the spread mode's partials: one wavefront per (sequence, head) and
+// per workgroup (a small batch has few of them: one CU each, since one CU
+// moves partials as slowly as cache rows), two output columns per lane; slots b * spread + r for
+// the sequence's non-empty shares (one share or none: written directly by the
+// decode kernel, skipped here).  The loads of kSpreadMergeBatch partials are
+// issued unconditionally, so they are all in flight together: the merge costs
+// one memory round trip per batch, not one per partial.
+constexpr int kSpreadMergeBatch = 32;
+
+__global__ __launch_bounds__(64) void decode_spread_merge_kernel(DecodeParams p) {
+  const int b = blockIdx.x / p.num_heads;
+  const int h = blockIdx.x - b * p.num_heads;
+  const int lane = threadIdx.x;
+  const int64_t first = static_cast<int64_t>(b) * p.spread;
+  const int col = 2 * lane < p.head_dim ? 2 * lane : 0;  // lane owns output columns col, col + 1
+  // The first batch's loads do not wait for the context length: slots of
+  // shares this launch left empty hold stale partials and are not folded.
+  f32x2 ml[kSpreadMergeBatch], v[kSpreadMergeBatch];
+  auto load_batch = [&](int s0) {
+#pragma unroll
+    for (int u = 0; u < kSpreadMergeBatch; ++u) {
+      const int64_t idx = (first + min(s0 + u, p.spread - 1)) * p.num_heads + h;
+      ml[u] = *reinterpret_cast<const f32x2*>(p.ws_ml + idx * 2);
+      v[u] = *reinterpret_cast<const f32x2*>(p.ws_o + idx * p.head_dim + col);
+    }
+  };
+  load_batch(0);
+  int per, shares;
+  spread_shares((clamped_len(p, b) + 31) >> 5, p.spread, per, shares);
+  if (shares <= 1) return;  // written directly by the decode kernel
+  float M = kNegInf, L = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int s0 = 0;;) {
+    // the batch's maximum first, then every weight at once: no chain of
+    // dependent exponentials through the shares
+    float mx = kNegInf;
+#pragma unroll
+    for (int u = 0; u < kSpreadMergeBatch; ++u)
+      if (s0 + u < shares) mx = fmaxf(mx, ml[u][0]);
+    const float m_new = fmaxf(M, mx);
+    if (m_new != kNegInf) {  // otherwise no valid key so far
+      const float a = fast_exp2(M - m_new);  // 0 while M is still -inf
+      L *= a;
+      o0 *= a;
+      o1 *= a;
+#pragma unroll
+      for (int u = 0; u < kSpreadMergeBatch; ++u) {
+        if (s0 + u >= shares) continue;  // a stale slot: never read into the sums
+        const float w = fast_exp2(ml[u][0] - m_new);  // 0 for a share with no valid key (max -inf)
+        L += w * ml[u][1];
+        o0 += w * v[u][0];
+        o1 += w * v[u][1];
+      }
+      M = m_new;
+    }
+    s0 += kSpreadMergeBatch;
+    if (s0 >= shares) break;
+    load_batch(s0);
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  if (2 * lane >= p.head_dim) return;
+  uint32_t* orow = reinterpret_cast<uint32_t*>(p.out + b * p.out_row_stride + h * p.head_dim + 2 * lane);
+  *orow = pack_bf16x2(o0 * inv, o1 * inv);
+}
+
 // Launch shape per cache dtype, chosen by measurement on MI355X (config 3 /
 // config 5 shapes): waves per workgroup (kv heads sharing a key range), whether
 // the next step's loads are issued before the current step's math, and the
@@ -664,15 +815,18 @@ int decode_waves_per_group(int32_t num_kv_heads, int32_t kv_dtype) {
 DecodePlan plan_decode(int32_t batch, int32_t num_kv_heads, int32_t max_blocks, int32_t block_size,
                        int32_t kv_dtype, int32_t requested_splits) {
   DecodePlan plan{};
-  // small batch, short table: the workgroup split (no workspace, no merge launch)
-  const int64_t table_keys = static_cast<int64_t>(max_blocks) * block_size;
-  if (requested_splits == 0 && static_cast<int64_t>(batch) * num_kv_heads <= kWgMaxGroups &&
-      table_keys <= int64_t{32} * kWgMaxStepsPerWave * kWgWaves) {
+  // small batch, short table: spread over many CUs, merged in the same launch
+  const int64_t table_steps = (static_cast<int64_t>(max_blocks) * block_size + 31) / 32;
+  const int64_t pairs = static_cast<int64_t>(batch) * num_kv_heads;
+  if (requested_splits == 0 && pairs <= kSpreadMaxPairs && max_blocks <= kWgMaxBlocks) {
+    int64_t S = kSpreadTargetWaves / pairs;
+    if (S > table_steps) S = table_steps;
+    if (S < 1) S = 1;
     plan.pages_per_split = max_blocks;
     plan.num_splits = 1;
     plan.balanced_ranges = 0;
-    plan.wg_split = 1;
-    plan.partial_slots = 0;
+    plan.spread = static_cast<int32_t>(S);
+    plan.partial_slots = S > 1 ? static_cast<int64_t>(batch) * S : 0;
     return plan;
   }
   if (requested_splits < 0) requested_splits = 0;  // -1: balanced whatever the sizes
@@ -717,10 +871,15 @@ static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
   else                                                                                                  \
     hipLaunchKernelGGL((KERNEL<FP8, 1, PF, D>), GRID, dim3(64), 0, stream, p);
   bool merge;
-  if (p.wg_split) {
-    const dim3 grid(static_cast<unsigned>(p.num_kv_heads), static_cast<unsigned>(p.batch));
-    hipLaunchKernelGGL((paged_decode_wgsplit_kernel<FP8, D>), grid, dim3(64 * kWgWaves), 0, stream, p);
-    merge = false;
+  if (p.spread > 0) {
+    const dim3 grid(static_cast<unsigned>(p.spread), static_cast<unsigned>(p.num_kv_heads),
+                    static_cast<unsigned>(p.batch));
+    hipLaunchKernelGGL((paged_decode_spread_kernel<FP8, D>), grid, dim3(64), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.spread == 1) return e;
+    hipLaunchKernelGGL(decode_spread_merge_kernel, dim3(static_cast<unsigned>(p.batch * p.num_heads)), dim3(64), 0,
+                       stream, p);
+    return hipGetLastError();
   } else if (p.balanced_ranges > 0) {
     const dim3 grid(static_cast<unsigned>(p.balanced_ranges), groups);
     NVA_LAUNCH_W(paged_decode_balanced_kernel, grid);

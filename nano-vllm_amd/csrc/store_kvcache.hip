@@ -19,18 +19,25 @@ namespace nva {
 template <int VB>
 __global__ __launch_bounds__(256) void store_kvcache_bf16_kernel(StoreParams p) {
   const int64_t t = blockIdx.x;
-  const int64_t slot = p.slot_mapping[t];
-  if (slot < 0 || slot >= p.num_slots) return;
   const int row_bytes = p.row_elems * 2;
   const int pieces = row_bytes / VB;
   const char* ksrc = static_cast<const char*>(p.key) + t * p.key_row_stride * 2;
   const char* vsrc = static_cast<const char*>(p.value) + t * p.value_row_stride * 2;
-  char* kdst = static_cast<char*>(p.k_cache) + slot * row_bytes;
-  char* vdst = static_cast<char*>(p.v_cache) + slot * row_bytes;
   // threadIdx.y selects key (0) or value (1)
   const char* src = threadIdx.y ? vsrc : ksrc;
+  // The first 16-byte piece is loaded together with the slot (the source row
+  // does not depend on it): a small batch then waits for one memory round trip
+  // before its stores instead of two.
+  const int c0 = threadIdx.x;
+  u32x4 first = {0u, 0u, 0u, 0u};
+  if (VB == 16 && c0 < pieces) first = ld16(src + c0 * 16);
+  const int64_t slot = p.slot_mapping[t];
+  if (slot < 0 || slot >= p.num_slots) return;
+  char* kdst = static_cast<char*>(p.k_cache) + slot * row_bytes;
+  char* vdst = static_cast<char*>(p.v_cache) + slot * row_bytes;
   char* dst = threadIdx.y ? vdst : kdst;
-  for (int c = threadIdx.x; c < pieces; c += blockDim.x) {
+  if (VB == 16 && c0 < pieces) __builtin_nontemporal_store(first, reinterpret_cast<u32x4*>(dst + c0 * 16));
+  for (int c = VB == 16 ? c0 + blockDim.x : c0; c < pieces; c += blockDim.x) {
     if constexpr (VB == 16) {
       __builtin_nontemporal_store(ld16(src + c * 16), reinterpret_cast<u32x4*>(dst + c * 16));
     } else if constexpr (VB == 8) {

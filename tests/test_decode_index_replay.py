@@ -243,3 +243,63 @@ def test_balanced_decode_indices_many_shapes(B, lo, hi):
                                   table_width=width)
         case.k_cache = torch.empty((pool, 256, nkv, d), dtype=torch.uint8, device="meta")
         replay(case, fp8, d, two)
+
+
+# ---------------------------------------------------------------------------
+# Spread mode (paged_decode_spread_kernel, plan_decode's small-batch branch).
+K_SPREAD_MAX_PAIRS, K_SPREAD_TARGET, K_MAX_BLOCKS = 256, 1024, 64
+
+
+def spread_plan(batch, nkv, max_blocks, block_size):
+    pairs = batch * nkv
+    if pairs > K_SPREAD_MAX_PAIRS or max_blocks > K_MAX_BLOCKS:
+        return None
+    table_steps = (max_blocks * block_size + 31) // 32
+    return max(1, min(K_SPREAD_TARGET // pairs, table_steps))
+
+
+def replay_spread(lengths, nh, nkv, D, max_blocks, block_size):
+    B = len(lengths)
+    S = spread_plan(B, nkv, max_blocks, block_size)
+    assert S is not None
+    G = nh // nkv
+    rows = B * S * nh if S > 1 else 0  # workspace rows: partial_slots * nh
+    for b, L in enumerate(lengths):
+        ctx = max(0, min(L, max_blocks * block_size))
+        steps = (ctx + 31) >> 5
+        per = (steps + S - 1) // S if steps > 0 else 1
+        shares = (steps + per - 1) // per
+        direct = shares <= 1
+        covered = []
+        for kvh in range(nkv):
+            for r in range(S):  # grid.x
+                if r >= (1 if direct else shares):
+                    continue
+                k0, k1 = min(ctx, 32 * per * r), min(ctx, 32 * per * (r + 1))
+                assert direct or k1 > k0, "a counted share must hold keys"
+                if kvh == 0:
+                    covered += list(range(k0, k1))
+                for key0 in range(k0, k1, 32):
+                    assert key0 // block_size < max_blocks <= 64  # readlane of the hoisted row
+                if not direct:
+                    slot = b * S + r
+                    for n in range(G):
+                        idx = slot * nh + kvh * G + n
+                        assert (idx + 1) * D <= rows * D and (idx + 1) * 2 <= rows * 2
+            if not direct:  # decode_merge_kernel reads shares 0 .. shares-1
+                for s in range(shares):
+                    assert (b * S + s + 1) * nh * D <= rows * D
+        assert covered == list(range(ctx)), f"sequence {b}: keys covered once, in order"
+    return S
+
+
+@pytest.mark.parametrize("nh,nkv,d", [(16, 8, 128), (14, 2, 64), (8, 1, 128), (128, 8, 128)])
+def test_spread_decode_indices(nh, nkv, d):
+    for B in (1, 3, 256 // nkv):
+        g = torch.Generator().manual_seed(B * 31 + nh)
+        for bs, width in ((256, 16), (64, 64), (32, 5), (256, 64)):
+            lengths = torch.randint(0, width * bs + 40, (B,), generator=g).tolist()
+            lengths[0] = width * bs
+            if B > 2:
+                lengths[1], lengths[2] = 0, 1
+            replay_spread(lengths, nh, nkv, d, width, bs)

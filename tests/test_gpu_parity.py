@@ -216,11 +216,11 @@ def test_decode_balanced_partition(dev, lengths, width, fp8):
 @pytest.mark.parametrize("nh,nkv,d", [(16, 8, 128), (32, 8, 128), (128, 8, 128), (8, 1, 128), (14, 2, 64),
                                       (16, 8, 64)])
 @pytest.mark.parametrize("fp8", [False, True])
-def test_decode_workgroup_split(dev, nh, nkv, d, fp8):
-    """The small-batch workgroup split (8 waves share a sequence's steps and merge
-    in LDS): ragged lengths incl. 0, 1 and a full 16-page table, at batches of 1 to
-    the largest it serves (batch * nkv = 256), against the oracle and the balanced
-    mode."""
+def test_decode_spread(dev, nh, nkv, d, fp8):
+    """The small-batch spread mode (one wave per share of a sequence's steps, the
+    partials merged by decode_merge_kernel): ragged lengths incl. 0, 1 and a full
+    16-page table, at batches of 1 to the largest it serves (batch * nkv = 256),
+    against the oracle and the balanced mode; a second call gives the same bits."""
     if fp8 and d != 128:
         pytest.skip("fp8 decode supports head_dim 128 only (nva_decode refuses it)")
     from nanovllm_amd import workloads as W
@@ -233,10 +233,11 @@ def test_decode_workgroup_split(dev, nh, nkv, d, fp8):
             lengths[1], lengths[2] = 0, 1
         case = W.make_decode_case(B, nh, nkv, 0, 0, 16 * B + 1, fp8=fp8, seed=B * 7 + nh, head_dim=d,
                                   bulk_device=dev, lengths=lengths, table_width=16)
-        assert _capi.load().nva_decode_workspace_bytes(B, nh, nkv, d, 16, 256, int(fp8), 0) == 0
+        assert _capi.load().nva_decode_workspace_bytes(B, nh, nkv, d, 16, 256, int(fp8), 0) > 0
         got = _run_decode(case, 0, store=False)
         tol = dict(max_abs=FP8_MAX_ABS, mean_abs=FP8_MAX_ABS) if fp8 else {}
-        assert_attn_close(got, decode_reference(case), what=f"wg split B={B} nh={nh} nkv={nkv} d={d}", **tol)
+        assert_attn_close(got, decode_reference(case), what=f"spread B={B} nh={nh} nkv={nkv} d={d}", **tol)
+        assert np.array_equal(_run_decode(case, 0, store=False), got)
         bal = _run_decode(case, -1, store=False)
         assert np.abs(got - bal).max() <= 1e-2
         for b, L in enumerate(lengths):
@@ -594,8 +595,8 @@ def test_decode_head_dim_64(dev, nh, nkv, fp8):
 
 @pytest.mark.skip(reason="the two-wave workgroup shape of the balanced decode (used for two kv heads) returned an "
                          "illegal address once (cause not found); it is no longer launched -- 14/2 decode runs one "
-                         "wave per workgroup or the workgroup split (golden decode_d64_g7, "
-                         "test_decode_workgroup_split) -- and this test stays skipped until that fault has a cause")
+                         "wave per workgroup or the spread mode (golden decode_d64_g7, "
+                         "test_decode_spread) -- and this test stays skipped until that fault has a cause")
 @pytest.mark.parametrize("head_dim", [64, 128])
 def test_decode_two_kv_heads(dev, head_dim):
     """Qwen2-0.5B heads 14/2 (qwen2_05b.txt:10,16,18)."""
