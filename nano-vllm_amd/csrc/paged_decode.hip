@@ -379,7 +379,7 @@ __device__ __forceinline__ void segment_accumulate(const DecodeParams& p, int kv
 // One wave, one kv head: attention of the head group's queries over keys
 // [k_begin, k_end) of sequence b.  Writes the normalised output when `direct`,
 // otherwise the unnormalised partial (O * v_scale, running max, sum) at `slot`.
-template <bool FP8, bool PREFETCH, int D>
+template <bool FP8, bool PREFETCH, int D, bool BUF = false>
 __device__ __forceinline__ void decode_segment(const DecodeParams& p, int kvh, int b, int k_begin, int k_end,
                                                bool direct, int64_t slot) {
   const int lane = threadIdx.x & 63;
@@ -389,7 +389,7 @@ __device__ __forceinline__ void decode_segment(const DecodeParams& p, int kvh, i
   const bool head_ok = n < p.group;
   f32x4 acc[8];
   float m_run, l;
-  segment_accumulate<FP8, PREFETCH, D>(p, kvh, b, k_begin, k_end, acc, m_run, l);
+  segment_accumulate<FP8, PREFETCH, D, false, BUF>(p, kvh, b, k_begin, k_end, acc, m_run, l);
   const float vscale = FP8 ? p.v_scale[kvh] : 1.0f;
   if (!head_ok || 32 * g >= D) return;  // lanes g >= D/32 hold no output columns
   if (direct) {
@@ -428,6 +428,29 @@ __device__ __forceinline__ int clamped_len(const DecodeParams& p, int b) {
   const int cap = p.max_blocks * p.block_size;
   return ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
 }
+
+// Launch shape per cache dtype, chosen by measurement on MI355X (config 3 /
+// config 5 shapes): waves per workgroup (kv heads sharing a key range), whether
+// the next step's loads are issued before the current step's math, and the
+// total number of waves the balanced mode spreads the steps over.
+//   bf16: 4 waves, prefetch (256 VGPRs, one wave per SIMD), 1024 waves
+//   fp8 : 8 waves, no prefetch (half the bytes per step), 2048 waves
+template <bool FP8>
+struct DecodeShape;
+template <>
+struct DecodeShape<false> {
+  static constexpr int kWaves = 4;
+  static constexpr bool kPrefetch = true;
+  static constexpr bool kBuf = true;  // buffer-resource steps, two in flight (-1.4% at config 3)
+  static constexpr int kTargetWaves = 1024;
+};
+template <>
+struct DecodeShape<true> {
+  static constexpr int kWaves = 8;
+  static constexpr bool kPrefetch = false;
+  static constexpr bool kBuf = false;  // the buffer pipeline measured +0.8% at config 5
+  static constexpr int kTargetWaves = 2048;
+};
 
 // ---------------------------------------------------------------------------
 // Fixed split-K: workgroup = WAVES kv heads of one sequence over one split of
@@ -585,7 +608,8 @@ __global__ __launch_bounds__(64 * WAVES) void paged_decode_balanced_kernel(Decod
   __shared__ int s_wsum[WAVES];
   __shared__ int s_seg[3 * CH];   // (b, first step, end step) of the chunk's pieces
   const int tid = threadIdx.x;
-  const int kvh = blockIdx.y * WAVES + (tid >> 6);
+  // wave-uniform (readfirstlane): the step buffer resources stay in scalar registers
+  const int kvh = __builtin_amdgcn_readfirstlane(blockIdx.y * WAVES + (tid >> 6));
   const int r = blockIdx.x;
   const int B = p.batch;
   const bool write_prefix = blockIdx.x == 0 && blockIdx.y == 0;
@@ -627,13 +651,13 @@ __global__ __launch_bounds__(64 * WAVES) void paged_decode_balanced_kernel(Decod
     __syncthreads();
     if (kvh < p.num_kv_heads) {
       for (int i = 0; i < nseg; ++i) {
-        const int sb = s_seg[3 * i];
-        const int lo = s_seg[3 * i + 1];
-        const int hi = s_seg[3 * i + 2];
-        const int len = clamped_len(p, sb);
+        const int sb = __builtin_amdgcn_readfirstlane(s_seg[3 * i]);
+        const int lo = __builtin_amdgcn_readfirstlane(s_seg[3 * i + 1]);
+        const int hi = __builtin_amdgcn_readfirstlane(s_seg[3 * i + 2]);
+        const int len = __builtin_amdgcn_readfirstlane(clamped_len(p, sb));
         const bool whole = lo == 0 && hi == ((len + 31) >> 5);
-        decode_segment<FP8, PREFETCH, D>(p, kvh, sb, 32 * lo, min(32 * hi, len), whole,
-                                         static_cast<int64_t>(sb) + r);
+        decode_segment<FP8, PREFETCH, D, DecodeShape<FP8>::kBuf>(p, kvh, sb, 32 * lo, min(32 * hi, len), whole,
+                                                                 static_cast<int64_t>(sb) + r);
       }
     }
     __syncthreads();  // s_seg is rewritten by the next chunk
@@ -781,27 +805,6 @@ __global__ __launch_bounds__(64) void decode_spread_merge_kernel(DecodeParams p)
   uint32_t* orow = reinterpret_cast<uint32_t*>(p.out + b * p.out_row_stride + h * p.head_dim + 2 * lane);
   *orow = pack_bf16x2(o0 * inv, o1 * inv);
 }
-
-// Launch shape per cache dtype, chosen by measurement on MI355X (config 3 /
-// config 5 shapes): waves per workgroup (kv heads sharing a key range), whether
-// the next step's loads are issued before the current step's math, and the
-// total number of waves the balanced mode spreads the steps over.
-//   bf16: 4 waves, prefetch (256 VGPRs, one wave per SIMD), 1024 waves
-//   fp8 : 8 waves, no prefetch (half the bytes per step), 2048 waves
-template <bool FP8>
-struct DecodeShape;
-template <>
-struct DecodeShape<false> {
-  static constexpr int kWaves = 4;
-  static constexpr bool kPrefetch = true;
-  static constexpr int kTargetWaves = 1024;
-};
-template <>
-struct DecodeShape<true> {
-  static constexpr int kWaves = 8;
-  static constexpr bool kPrefetch = false;
-  static constexpr int kTargetWaves = 2048;
-};
 
 // The two-wave shape is not used: with two kv heads it returned an illegal
 // address on the GPU once and unnormalised garbage (fp8) in another run, for
