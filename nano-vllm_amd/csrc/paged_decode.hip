@@ -748,8 +748,11 @@ __global__ __launch_bounds__(64 * kMergeHeads) void decode_merge_kernel(DecodePa
 // the sequence's non-empty shares (one share or none: written directly by the
 // decode kernel, skipped here).  The loads of kSpreadMergeBatch partials are
 // issued unconditionally, so they are all in flight together: the merge costs
-// one memory round trip per batch, not one per partial.
-constexpr int kSpreadMergeBatch = 32;
+// one memory round trip per batch, not one per partial.  16 per batch: a
+// small-batch step is latency-bound and this kernel's code is fetched cold by
+// each CU, so a 32-way unrolled batch (twice the code) measured slower
+// (captured batch 1: 12.6 vs 13.1 us per layer; batch 16: 22.4 vs 24.0).
+constexpr int kSpreadMergeBatch = 16;
 
 __global__ __launch_bounds__(64) void decode_spread_merge_kernel(DecodeParams p) {
   const int b = blockIdx.x / p.num_heads;
