@@ -9,6 +9,8 @@
  *   nva_decode         <- flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
  *                         cache_seqlens, block_table, softmax_scale,
  *                         causal=True)                             attention.py:74-77
+ * plus the decode branch of Attention.forward as one call (store, then decode):
+ *   nva_store_decode   <- store_kvcache + flash_attn_with_kvcache    attention.py:58-79
  * and one fused producer step just before attention:
  *   nva_qk_norm_rope   <- q_norm / k_norm + rotary_emb             qwen3.py:91-105
  *
@@ -140,6 +142,34 @@ int nva_decode(const void* q, int64_t q_row_stride,
                float softmax_scale, int32_t num_splits,
                void* out, int64_t out_row_stride,
                void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * One decode step of Attention.forward (attention.py:58-79, decode branch): the store of the
+ * new token's key/value rows (store_kvcache, attention.py:32-39 / 10-29) followed by the paged
+ * decode (flash_attn_with_kvcache, attention.py:75-77).  key/value: (batch, num_kv_heads,
+ * head_dim) bf16 rows at key_row_stride / value_row_stride; slot_mapping: (batch,) int32, slots
+ * outside [0, num_blocks*block_size) skipped; every other argument as nva_decode (same workspace,
+ * nva_decode_workspace_bytes).  It has no single counterpart in the reference.
+ * When nva_decode's plan is the small-batch spread mode, the store runs inside the decode launch:
+ * the workgroup that reads key cache_seqlens[b]-1 writes the new rows and uses them from registers.
+ * That equals store-then-decode when slot_mapping[b] is the slot of key cache_seqlens[b]-1 of
+ * sequence b (as every decode step the reference runs has it: prepare_decode, model_runner.py
+ * :218-229) and no other sequence of the batch reads that slot; otherwise the attention over the
+ * new token's slot is unspecified (the store itself is done).  Other plans run the store kernel,
+ * then the decode.
+ */
+int nva_store_decode(const void* key, int64_t key_row_stride,
+                     const void* value, int64_t value_row_stride,
+                     const int32_t* slot_mapping,
+                     const void* q, int64_t q_row_stride,
+                     void* k_cache, void* v_cache, int32_t kv_dtype,
+                     const float* k_scale, const float* v_scale, int64_t num_blocks,
+                     const int32_t* cache_seqlens, const int32_t* block_table,
+                     int64_t bt_row_stride, int32_t max_blocks_per_seq, int32_t block_size,
+                     int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                     float softmax_scale, int32_t num_splits,
+                     void* out, int64_t out_row_stride,
+                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Gather each sequence's keys and values from the paged caches into packed bf16 rows:

@@ -49,11 +49,16 @@ int nva_version(void) { return 100; }
 
 const char* nva_last_error(void) { return g_last_error.c_str(); }
 
-int nva_store_kvcache(const void* key, int64_t key_row_stride, const void* value,
-                      int64_t value_row_stride, void* k_cache, void* v_cache, int64_t num_slots,
-                      const int32_t* slot_mapping, int64_t num_tokens, int32_t num_kv_heads,
-                      int32_t head_dim, int32_t cache_dtype, const float* k_scale,
-                      const float* v_scale, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Validate a store and fill its parameters and vector width (the launch is
+// the caller's).  Shared by nva_store_kvcache and nva_store_decode.
+int store_setup(const void* key, int64_t key_row_stride, const void* value, int64_t value_row_stride,
+                void* k_cache, void* v_cache, int64_t num_slots, const int32_t* slot_mapping, int64_t num_tokens,
+                int32_t num_kv_heads, int32_t head_dim, int32_t cache_dtype, const float* k_scale,
+                const float* v_scale, nva::StoreParams& p, int& vec) {
   if (num_tokens < 0) return fail(NVA_ERR_INVALID_ARGUMENT, "num_tokens must be >= 0 (got %lld)", (long long)num_tokens);
   if (num_tokens > 0x7fffffffLL) return fail(NVA_ERR_UNSUPPORTED, "num_tokens above 2^31-1");
   if (num_kv_heads <= 0 || head_dim <= 0)
@@ -71,7 +76,7 @@ int nva_store_kvcache(const void* key, int64_t key_row_stride, const void* value
   if (D > (1 << 20)) return fail(NVA_ERR_UNSUPPORTED, "num_kv_heads*head_dim above 2^20");
   if (!aligned(slot_mapping, 4)) return fail(NVA_ERR_INVALID_ARGUMENT, "slot_mapping must be 4-byte aligned");
 
-  nva::StoreParams p{};
+  p = nva::StoreParams{};
   p.key = key;
   p.value = value;
   p.k_cache = k_cache;
@@ -87,7 +92,7 @@ int nva_store_kvcache(const void* key, int64_t key_row_stride, const void* value
   p.head_dim = head_dim;
   p.cache_dtype = cache_dtype;
 
-  int vec = 2;
+  vec = 2;
   if (cache_dtype == NVA_DTYPE_FP8_E4M3) {
     if (!k_scale || !v_scale) return fail(NVA_ERR_INVALID_ARGUMENT, "fp8 cache needs k_scale and v_scale");
     if (head_dim % 8 != 0) return fail(NVA_ERR_UNSUPPORTED, "fp8 store needs head_dim %% 8 == 0");
@@ -107,6 +112,23 @@ int nva_store_kvcache(const void* key, int64_t key_row_stride, const void* value
     if (!aligned(key, 2) || !aligned(value, 2) || !aligned(k_cache, 2) || !aligned(v_cache, 2))
       return fail(NVA_ERR_INVALID_ARGUMENT, "bf16 tensors must be 2-byte aligned");
   }
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int nva_store_kvcache(const void* key, int64_t key_row_stride, const void* value,
+                      int64_t value_row_stride, void* k_cache, void* v_cache, int64_t num_slots,
+                      const int32_t* slot_mapping, int64_t num_tokens, int32_t num_kv_heads,
+                      int32_t head_dim, int32_t cache_dtype, const float* k_scale,
+                      const float* v_scale, void* stream) {
+  nva::StoreParams p{};
+  int vec = 2;
+  const int rc = store_setup(key, key_row_stride, value, value_row_stride, k_cache, v_cache, num_slots, slot_mapping,
+                             num_tokens, num_kv_heads, head_dim, cache_dtype, k_scale, v_scale, p, vec);
+  if (rc != NVA_OK || num_tokens == 0) return rc;
   return hip_status(nva::launch_store_kvcache(p, vec, static_cast<hipStream_t>(stream)), "store_kvcache launch");
 }
 
@@ -248,7 +270,8 @@ int decode_impl(const void* q, int64_t q_row_stride, const void* k_cache, const 
                 const int32_t* block_table, int64_t bt_row_stride, int32_t max_blocks_per_seq, int32_t block_size,
                 int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
                 int32_t num_splits, void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
-                void* stream, int64_t scratch_max, void* (*get_scratch)()) {
+                void* stream, int64_t scratch_max, void* (*get_scratch)(),
+                const nva::StoreParams* store = nullptr, int store_vec = 0) {
   if (head_dim != 128 && head_dim != 64)
     return fail(NVA_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", head_dim);
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
@@ -339,6 +362,20 @@ int decode_impl(const void* q, int64_t q_row_stride, const void* k_cache, const 
   p.spread = plan.spread;
   p.head_dim = head_dim;
   p.scale_log2 = softmax_scale * kLog2e;
+  if (store) {
+    // The spread mode stores inside its own launch (16-byte source pieces);
+    // otherwise the store kernel runs first.
+    if (plan.spread > 0 && (kv_dtype == NVA_DTYPE_FP8_E4M3 || store_vec == 16)) {
+      p.new_k = static_cast<const uint16_t*>(store->key);
+      p.new_v = static_cast<const uint16_t*>(store->value);
+      p.new_k_stride = store->key_row_stride;
+      p.new_v_stride = store->value_row_stride;
+      p.slot_mapping = store->slot_mapping;
+    } else {
+      const hipError_t e = nva::launch_store_kvcache(*store, store_vec, static_cast<hipStream_t>(stream));
+      if (e != hipSuccess) return hip_status(e, "store_kvcache launch");
+    }
+  }
   return hip_status(nva::launch_decode(p, kv_dtype, static_cast<hipStream_t>(stream)), "decode launch");
 }
 
@@ -356,6 +393,26 @@ int nva_decode(const void* q, int64_t q_row_stride, const void* k_cache, const v
                      block_table, bt_row_stride, max_blocks_per_seq, block_size, batch, num_heads, num_kv_heads,
                      head_dim, softmax_scale, num_splits, out, out_row_stride, workspace, workspace_bytes, stream, 0,
                      nullptr);
+}
+
+int nva_store_decode(const void* key, int64_t key_row_stride, const void* value, int64_t value_row_stride,
+                     const int32_t* slot_mapping, const void* q, int64_t q_row_stride, void* k_cache, void* v_cache,
+                     int32_t kv_dtype, const float* k_scale, const float* v_scale, int64_t num_blocks,
+                     const int32_t* cache_seqlens, const int32_t* block_table, int64_t bt_row_stride,
+                     int32_t max_blocks_per_seq, int32_t block_size, int32_t batch, int32_t num_heads,
+                     int32_t num_kv_heads, int32_t head_dim, float softmax_scale, int32_t num_splits, void* out,
+                     int64_t out_row_stride, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (num_blocks <= 0 || block_size <= 0 || num_blocks > INT64_MAX / block_size)
+    return fail(NVA_ERR_INVALID_ARGUMENT, "num_blocks and block_size must be positive");
+  nva::StoreParams sp{};
+  int vec = 2;
+  const int rc = store_setup(key, key_row_stride, value, value_row_stride, k_cache, v_cache, num_blocks * block_size,
+                             slot_mapping, batch, num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, sp, vec);
+  if (rc != NVA_OK) return rc;
+  return decode_impl(q, q_row_stride, k_cache, v_cache, kv_dtype, k_scale, v_scale, num_blocks, cache_seqlens,
+                     block_table, bt_row_stride, max_blocks_per_seq, block_size, batch, num_heads, num_kv_heads,
+                     head_dim, softmax_scale, num_splits, out, out_row_stride, workspace, workspace_bytes, stream, 0,
+                     nullptr, batch > 0 ? &sp : nullptr, vec);
 }
 
 int64_t nva_decode_noalloc_max_workspace_bytes(void) { return kDecodeScratchBytes; }

@@ -74,6 +74,50 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __builtin_bit_cast(float, bits16 << 16);
 }
 
+// f32 -> OCP e4m3fn with round-to-nearest-even on the grid extended by 480
+// (the NaN code 0x7f): magnitudes above 464, the midpoint of 448 and 480, and
+// infinities and NaNs map to NaN (0x7f) with the input's sign bit; exactly 464
+// ties to even (448).
+//  - |x| < 2^-6 (the subnormal range): adding 2^14 rounds |x| to a multiple of
+//    2^-9, the subnormal step, and the low mantissa bits of the sum are the code.
+//  - otherwise: round the 23-bit mantissa to 3 bits (ties to even) and rebias
+//    the exponent from 127 to 7.
+__device__ __forceinline__ uint32_t f32_to_e4m3fn(float x) {
+  uint32_t bits = __builtin_bit_cast(uint32_t, x);
+  const uint32_t sign = (bits >> 24) & 0x80u;
+  bits &= 0x7fffffffu;
+  uint32_t code;
+  if (bits > 0x43e80000u) {  // > 464.0f, inf or NaN
+    code = 0x7fu;
+  } else if (bits < 0x3c800000u) {  // < 2^-6
+    const float y = __builtin_bit_cast(float, bits) + 16384.0f;
+    code = __builtin_bit_cast(uint32_t, y) - 0x46800000u;
+  } else {
+    const uint32_t odd = (bits >> 20) & 1u;
+    bits += 0x7ffffu + odd;
+    code = (bits >> 20) - (120u << 3);
+  }
+  return code | sign;
+}
+
+// Eight bf16 values (16 bytes, element e in bits 16 (e % 2) of word e / 2)
+// divided by `scale`, as eight e4m3fn codes (8 bytes, code e in byte e).
+__device__ __forceinline__ u32x2 bf16x8_to_e4m3fn(u32x4 w, float scale) {
+  u32x2 out;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t word = w[2 * h + (e >> 1)];
+      const uint32_t b16 = (e & 1) ? (word >> 16) : (word & 0xffffu);
+      packed |= f32_to_e4m3fn(bf16_bits_to_f32(b16) / scale) << (8 * e);
+    }
+    out[h] = packed;
+  }
+  return out;
+}
+
 // Two e4m3fn bytes (selected 16-bit half of `w`) -> two bf16 in one dword.
 // The conversion is exact: every e4m3fn value is representable in bf16.
 template <bool HI>

@@ -51,6 +51,13 @@ struct DecodeParams {
   int32_t balanced_ranges;    // balanced mode: number of step ranges P (0 = fixed mode)
   int32_t spread;             // > 0: spread mode with that many shares per sequence (small batches)
   int32_t head_dim;           // 64 or 128
+  // Store fused into the spread launch (null new_k: none): row b of new_k /
+  // new_v (bf16, nkv * d elements) goes to cache slot slot_mapping[b].
+  const uint16_t* new_k;
+  const uint16_t* new_v;
+  int64_t new_k_stride;
+  int64_t new_v_stride;
+  const int32_t* slot_mapping;
   float scale_log2;           // softmax_scale * log2(e)
 };
 

@@ -291,13 +291,94 @@ __device__ __forceinline__ void compute_step(StepRegs<FP8>& r, int nvalid, int g
   }
 }
 
+// No register patch (every caller but the fused store).
+struct NoPatch {
+  template <class R>
+  __device__ __forceinline__ void apply(R&, int) const {}
+};
+
+// The new token's key and value of one kv head, as this lane holds them in a
+// step's registers (StepRegs layout), and where they go: local step `step`
+// of the segment, row `row` of that step (step -1: nowhere).  The spread
+// kernel with a fused store patches them into the step's freshly loaded
+// registers instead of waiting for its own store to reach the cache.  The
+// bf16 source pieces are kept as loaded; fp8 quantises them (as the store
+// does) only in the patched step, so no wait for them precedes the step loads.
+template <bool FP8, int D>
+struct NewRow {
+  static constexpr int NK = D / 32;  // 16-byte bf16 source pieces of the key row per lane
+  int step = -1;
+  int row = 0;
+  float ks = 1.f, vs = 1.f;
+  u32x4 k[NK];
+  u32x4 v;
+
+  // Source pieces for lane (n, g): bf16 K dims qk_dim(s, g) .. +7 (bf16
+  // cache) or 64 u + 16 g .. +15 (fp8 cache, pieces 2u and 2u+1); V columns
+  // 8 n .. 8 n + 7.
+  __device__ __forceinline__ void load(const uint16_t* kin, const uint16_t* vin, int n, int g, float kscale,
+                                       float vscale) {
+    ks = kscale;
+    vs = vscale;
+#pragma unroll
+    for (int s = 0; s < NK; ++s)
+      k[s] = ld16(kin + (FP8 ? 64 * (s >> 1) + 16 * g + 8 * (s & 1) : qk_dim<false>(s, g)));
+    v = ld16(vin + 8 * (D == 128 || n < D / 8 ? n : 0));
+  }
+
+  // Registers of local step i: the K tile row `row` lives in lanes
+  // n = 4 (row / 8) + row % 4 (tile t = row / 4 % 2), the V row in lanes
+  // g = row / 8 (register row % 8).
+  __device__ __forceinline__ void apply(StepRegs<FP8>& r, int i) const {
+    if (i != step) return;
+    const int lane = threadIdx.x & 63;
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int t = (row >> 2) & 1;
+    const bool kl = n == 4 * (row >> 3) + (row & 3);
+    const bool vl = g == (row >> 3);
+    if constexpr (!FP8) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int s = 0; s < NK; ++s) r.k[tt][s] = (tt == t && kl) ? k[s] : r.k[tt][s];
+      const u32x4 vv = D == 128 || n < D / 8 ? v : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int ii = 0; ii < 8; ++ii) r.v[ii] = (ii == (row & 7) && vl) ? vv : r.v[ii];
+    } else {
+      // the empty asm keeps the quantisation here (hoisted out of the step
+      // loop, it would wait for the source loads before the first step's loads)
+      u32x4 kk[NK];
+#pragma unroll
+      for (int s = 0; s < NK; ++s) {
+        kk[s] = k[s];
+        asm volatile("" : "+v"(kk[s]));
+      }
+      u32x4 vr = v;
+      asm volatile("" : "+v"(vr));
+#pragma unroll
+      for (int u = 0; u < D / 64; ++u) {
+        const u32x2 lo = bf16x8_to_e4m3fn(kk[2 * u], ks);
+        const u32x2 hi = bf16x8_to_e4m3fn(kk[2 * u + 1], ks);
+        const u32x4 c = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) r.k[tt][u] = (tt == t && kl) ? c : r.k[tt][u];
+      }
+      const u32x2 vc = bf16x8_to_e4m3fn(vr, vs);
+#pragma unroll
+      for (int ii = 0; ii < 8; ++ii) r.v[ii] = (ii == (row & 7) && vl) ? vc : r.v[ii];
+    }
+  }
+};
+
 // One wave, one kv head: the unnormalised attention state of the head group's
 // queries over keys [k_begin, k_end) of sequence b -- O^T in acc (lane (n, g):
 // head n, columns 32g .. 32g+31), the running maximum m_run (log2 units) and
 // the row sum `l` (summed over the four lanes of a head).
-template <bool FP8, bool PREFETCH, int D, bool HOIST = false, bool BUF = false>
+template <bool FP8, bool PREFETCH, int D, bool HOIST = false, bool BUF = false, class Patch = NoPatch>
 __device__ __forceinline__ void segment_accumulate(const DecodeParams& p, int kvh, int b, int k_begin, int k_end,
-                                                   f32x4 (&acc)[8], float& m_run, float& l, int bt_row = 0) {
+                                                   f32x4 (&acc)[8], float& m_run, float& l, int bt_row = 0,
+                                                   const Patch& patch = Patch{}) {
   constexpr int EB = FP8 ? 1 : 2;  // bytes per cache element
   const int lane = threadIdx.x & 63;
   const int n = lane & 15;
@@ -348,10 +429,14 @@ __device__ __forceinline__ void segment_accumulate(const DecodeParams& p, int kv
     for (int i = 0; i < nsteps; i += 2) {
       const StepRsrc rb = step_rsrc<HOIST, RB>(w, i + 1, nsteps, bt_row);
       load_step_buf<FP8, D>(B, w, rb);
+      patch.apply(A, i);
       compute_step<FP8, D, false>(A, ra.nvalid, g, qop, sl2, acc, m_run, l_run);
       ra = step_rsrc<HOIST, RB>(w, i + 2, nsteps, bt_row);
       load_step_buf<FP8, D>(A, w, ra);
-      if (i + 1 < nsteps) compute_step<FP8, D, false>(B, rb.nvalid, g, qop, sl2, acc, m_run, l_run);
+      if (i + 1 < nsteps) {
+        patch.apply(B, i + 1);
+        compute_step<FP8, D, false>(B, rb.nvalid, g, qop, sl2, acc, m_run, l_run);
+      }
     }
   } else if (nsteps > 0) {
     StepRegs<FP8> A, B;
@@ -493,7 +578,7 @@ __device__ __forceinline__ void spread_shares(int steps, int S, int& per, int& s
   shares = (steps + per - 1) / per;
 }
 
-template <bool FP8, int D>
+template <bool FP8, int D, bool STORE>
 __global__ __launch_bounds__(64) void paged_decode_spread_kernel(DecodeParams p) {
   const int r = blockIdx.x;
   const int kvh = blockIdx.y;
@@ -512,9 +597,52 @@ __global__ __launch_bounds__(64) void paged_decode_spread_kernel(DecodeParams p)
   const int k_end = min(ctx, 32 * per * (r + 1));
   f32x4 acc[8];
   float m_run, l;
-  segment_accumulate<FP8, true, D, true, true>(p, kvh, b, k_begin, k_end, acc, m_run, l, bt_row);
   const int n = lane & 15;
   const int g = lane >> 4;
+  if constexpr (STORE) {
+    // The share holding key ctx-1 (share 0 of an empty sequence) stores the
+    // new token's rows of this kv head.  When slot_mapping[b] is key ctx-1's
+    // slot -- what every decode step produces -- that share's own read of the
+    // key is patched from registers, so no other share reads the slot and
+    // the result equals store-then-decode without waiting for the store.
+    const int64_t slot = __builtin_amdgcn_readfirstlane(p.slot_mapping[b]);
+    const int holder = ctx > 0 ? (ctx - 1) / (32 * per) : 0;
+    NewRow<FP8, D> nr;
+    const bool stores = r == holder && slot >= 0 && slot < static_cast<int64_t>(p.num_blocks) * p.block_size;
+    // lanes 0..D/8-1 store the key row, lanes 32.. the value row, 8 elements
+    // each; the rows are loaded now and stored after the steps, so the store
+    // never holds up this share's own loads
+    const int j = lane & 31;
+    const bool is_v = lane >= 32;
+    u32x4 x = {0u, 0u, 0u, 0u};
+    if (stores) {
+      const uint16_t* kin = p.new_k + b * p.new_k_stride + kvh * D;
+      const uint16_t* vin = p.new_v + b * p.new_v_stride + kvh * D;
+      nr.load(kin, vin, n, g, FP8 ? p.k_scale[kvh] : 1.f, FP8 ? p.v_scale[kvh] : 1.f);
+      x = ld16((is_v ? vin : kin) + 8 * (j & (D / 8 - 1)));  // every lane loads (no branch), D/8 of them store
+      if (ctx > 0) {
+        const int key = ctx - 1;
+        const int blk = key / p.block_size;
+        const int page = __builtin_amdgcn_readlane(bt_row, blk);
+        if (static_cast<int64_t>(page) * p.block_size + (key - blk * p.block_size) == slot) {
+          nr.step = (key >> 5) - (k_begin >> 5);
+          nr.row = key & 31;
+        }
+      }
+    }
+    segment_accumulate<FP8, true, D, true, true>(p, kvh, b, k_begin, k_end, acc, m_run, l, bt_row, nr);
+    if (stores && j < D / 8) {
+      constexpr int EB = FP8 ? 1 : 2;
+      char* dst = static_cast<char*>(const_cast<void*>(is_v ? p.v_cache : p.k_cache)) +
+                  (slot * p.num_kv_heads + kvh) * D * EB + 8 * j * EB;
+      if constexpr (FP8)
+        *reinterpret_cast<u32x2*>(dst) = bf16x8_to_e4m3fn(x, is_v ? p.v_scale[kvh] : p.k_scale[kvh]);
+      else
+        *reinterpret_cast<u32x4*>(dst) = x;
+    }
+  } else {
+    segment_accumulate<FP8, true, D, true, true>(p, kvh, b, k_begin, k_end, acc, m_run, l, bt_row);
+  }
   const bool cols = n < p.group && 32 * g < D;  // lanes holding a head's output columns
   const int h = kvh * p.group + n;
   const float vscale = FP8 ? p.v_scale[kvh] : 1.0f;
@@ -880,7 +1008,10 @@ static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
   if (p.spread > 0) {
     const dim3 grid(static_cast<unsigned>(p.spread), static_cast<unsigned>(p.num_kv_heads),
                     static_cast<unsigned>(p.batch));
-    hipLaunchKernelGGL((paged_decode_spread_kernel<FP8, D>), grid, dim3(64), 0, stream, p);
+    if (p.new_k)
+      hipLaunchKernelGGL((paged_decode_spread_kernel<FP8, D, true>), grid, dim3(64), 0, stream, p);
+    else
+      hipLaunchKernelGGL((paged_decode_spread_kernel<FP8, D, false>), grid, dim3(64), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.spread == 1) return e;
     hipLaunchKernelGGL(decode_spread_merge_kernel, dim3(static_cast<unsigned>(p.batch * p.num_heads)), dim3(64), 0,

@@ -48,6 +48,17 @@ SIGNATURES = {
     ]),
     "nva_prefill_workspace_bytes": (_i64, []),
     "nva_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "nva_store_decode": (_i32, [
+        _c_void_p, _i64, _c_void_p, _i64,  # key, key_row_stride, value, value_row_stride
+        _c_void_p,                         # slot_mapping
+        _c_void_p, _i64,                   # q, q_row_stride
+        _c_void_p, _c_void_p, _i32,        # k_cache, v_cache, kv_dtype
+        _c_void_p, _c_void_p, _i64,        # k_scale, v_scale, num_blocks
+        _c_void_p, _c_void_p, _i64, _i32, _i32,  # seqlens, block_table, bt_row_stride, max_blocks, block_size
+        _i32, _i32, _i32, _i32, _f32, _i32,  # batch, nh, nkv, head_dim, scale, num_splits
+        _c_void_p, _i64,                   # out, out_row_stride
+        _c_void_p, _i64, _c_void_p,        # workspace, workspace_bytes, stream
+    ]),
     "nva_decode": (_i32, [
         _c_void_p, _i64,                   # q, q_row_stride
         _c_void_p, _c_void_p, _i32,        # k_cache, v_cache, kv_dtype

@@ -99,6 +99,19 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
     Same preconditions as the reference, raised as AssertionError like its asserts
     (attention.py:35-38).  Slots outside [0, num_blocks*block_size) are skipped.
     """
+    N, num_heads, head_dim, code = _check_store(key, value, k_cache, v_cache, slot_mapping, k_scale, v_scale)
+    num_slots = k_cache.numel() // (num_heads * head_dim)
+    lib = _capi.load()
+    _capi.check(lib.nva_store_kvcache(
+        key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+        k_cache.data_ptr(), v_cache.data_ptr(), num_slots,
+        slot_mapping.data_ptr(), N, num_heads, head_dim, code,
+        _ptr(k_scale), _ptr(v_scale), _stream(key)))
+
+
+def _check_store(key, value, k_cache, v_cache, slot_mapping, k_scale, v_scale):
+    """store_kvcache's preconditions (attention.py:35-38 asserts, then dtype,
+    layout and device checks); returns (N, num_kv_heads, head_dim, cache dtype code)."""
     N, num_heads, head_dim = key.shape
     D = num_heads * head_dim
     assert key.stride(-1) == 1 and value.stride(-1) == 1
@@ -117,13 +130,7 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
     _check_scales(code, k_scale, v_scale, num_heads, k_cache.device)
     _check_device(key.device, value=value, k_cache=k_cache, v_cache=v_cache, slot_mapping=slot_mapping,
                   k_scale=k_scale, v_scale=v_scale)
-    num_slots = k_cache.numel() // D
-    lib = _capi.load()
-    _capi.check(lib.nva_store_kvcache(
-        key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
-        k_cache.data_ptr(), v_cache.data_ptr(), num_slots,
-        slot_mapping.data_ptr(), N, num_heads, head_dim, code,
-        _ptr(k_scale), _ptr(v_scale), _stream(key)))
+    return N, num_heads, head_dim, code
 
 
 def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, max_seqlen_q: int,
@@ -217,6 +224,35 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     (0 = heuristic, n > 0 = about n splits per sequence), and -1 selects the
     balanced split-K whatever the sizes."""
     del causal
+    a = _decode_args(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale, num_splits, k_scale, v_scale)
+    _capi.check(_capi.load().nva_decode(*a["decode"], _stream(q)))
+    return a["out"]
+
+
+def store_and_decode(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                     v_cache: torch.Tensor, slot_mapping: torch.Tensor, cache_seqlens: torch.Tensor,
+                     block_table: torch.Tensor, softmax_scale: float | None = None, num_splits: int = 0,
+                     k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """The decode branch of Attention.forward as one call: store_kvcache of the new
+    rows (attention.py:32-39), then flash_attn_with_kvcache (attention.py:75-77).
+    Small batches run the store inside the decode launch (nva_store_decode); the
+    result equals the two calls when slot_mapping[b] is the slot of key
+    cache_seqlens[b]-1, as prepare_decode (model_runner.py:218-229) produces it."""
+    N = key.shape[0]
+    if N != q.shape[0]:
+        raise RuntimeError("one new key/value row per sequence")
+    _check_store(key, value, k_cache, v_cache, slot_mapping, k_scale, v_scale)
+    a = _decode_args(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale, num_splits, k_scale, v_scale)
+    _check_device(q.device, key=key, value=value, slot_mapping=slot_mapping)
+    _capi.check(_capi.load().nva_store_decode(
+        key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0), slot_mapping.data_ptr(),
+        *a["decode"], _stream(q)))
+    return a["out"]
+
+
+def _decode_args(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale, num_splits, k_scale, v_scale):
+    """Checks of the decode call and its nva_decode arguments (all but the stream),
+    with the output tensor and the workspace allocated."""
     if q.dim() != 4 or q.shape[1] != 1:
         raise RuntimeError("q must be (batch, 1, num_heads, head_dim)")
     B, _, nh, d = q.shape
@@ -246,13 +282,12 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     lib = _capi.load()
     ws_bytes = lib.nva_decode_workspace_bytes(B, nh, nkv, d, max_blocks, block_size, code, int(num_splits))
     ws = torch.empty(max(ws_bytes, 0), dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
-    _capi.check(lib.nva_decode(
-        q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), code,
-        _ptr(k_scale), _ptr(v_scale), num_blocks,
-        cache_seqlens.data_ptr(), block_table.data_ptr(), block_table.stride(0), max_blocks, block_size,
-        B, nh, nkv, d, float(softmax_scale), int(num_splits),
-        out.data_ptr(), out.stride(0), _ptr(ws), ws_bytes, _stream(q)))
-    return out
+    args = (q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), code,
+            _ptr(k_scale), _ptr(v_scale), num_blocks,
+            cache_seqlens.data_ptr(), block_table.data_ptr(), block_table.stride(0), max_blocks, block_size,
+            B, nh, nkv, d, float(softmax_scale), int(num_splits),
+            out.data_ptr(), out.stride(0), _ptr(ws), ws_bytes)
+    return {"decode": args, "out": out, "workspace": ws}
 
 
 class Attention(nn.Module):
@@ -274,7 +309,13 @@ class Attention(nn.Module):
         v = v.view(-1, self.num_kv_heads, self.head_dim)
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
-        if k_cache.numel() and v_cache.numel():
+        bound = k_cache.numel() and v_cache.numel()
+        if not context.is_prefill and bound:  # decode: store and attention as one call
+            o = store_and_decode(q.unsqueeze(1), k, v, k_cache, v_cache, context.slot_mapping,
+                                 context.context_lens, context.block_tables, softmax_scale=self.scale,
+                                 k_scale=self.k_scale, v_scale=self.v_scale)
+            return o.view(-1, self.num_heads * self.head_dim)
+        if bound:
             store_kvcache(k, v, k_cache, v_cache, context.slot_mapping, self.k_scale, self.v_scale)
         if context.is_prefill:
             if context.block_tables is not None:  # prefix cache

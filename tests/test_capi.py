@@ -179,6 +179,40 @@ def test_decode_workspace_plan(lib):
     assert f(0, 16, 8, 128, 8, 256, 0, 0) == 0
 
 
+def store_decode(lib, **kw):
+    st = dict(key=A + 0x100000, key_row_stride=1024, value=A + 0x180000, value_row_stride=1024,
+              slot_mapping=A + 0xB000)
+    dec = dict(q=A, q_row_stride=2048, k_cache=B, v_cache=C, kv_dtype=0, k_scale=None, v_scale=None,
+               num_blocks=2048, seqlens=A + 0x9000, block_table=A + 0xA000, bt_row_stride=8, max_blocks=8,
+               block_size=256, batch=256, num_heads=16, num_kv_heads=8, head_dim=128, scale=0.088,
+               num_splits=0, out=C + 0x200000, out_row_stride=2048, workspace=None, workspace_bytes=0,
+               stream=None)
+    for d in (st, dec):
+        for k in list(kw):
+            if k in d:
+                d[k] = kw.pop(k)
+    assert not kw, kw
+    return lib.nva_store_decode(*st.values(), *dec.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(key_row_stride=512), _capi.NVA_ERR_INVALID_ARGUMENT),      # < nkv * d
+    (dict(key=None), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(slot_mapping=A + 0xB002), _capi.NVA_ERR_INVALID_ARGUMENT),  # misaligned
+    (dict(kv_dtype=1), _capi.NVA_ERR_INVALID_ARGUMENT),              # fp8 without scales
+    (dict(num_blocks=0), _capi.NVA_ERR_INVALID_ARGUMENT),
+    (dict(head_dim=96, key_row_stride=768, value_row_stride=768), _capi.NVA_ERR_UNSUPPORTED),
+    (dict(workspace=A, workspace_bytes=16), _capi.NVA_ERR_WORKSPACE),
+])
+def test_store_decode_rejects(lib, kw, code):
+    """Both halves are validated (the store's, then the decode's) before any launch."""
+    assert store_decode(lib, **kw) == code
+
+
+def test_store_decode_batch_zero_is_noop(lib):
+    assert store_decode(lib, batch=0) == _capi.NVA_OK
+
+
 def test_decode_batch_zero_is_noop(lib):
     assert decode(lib, batch=0, workspace=None) == _capi.NVA_OK
 

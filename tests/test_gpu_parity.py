@@ -146,6 +146,39 @@ def test_decode_cfg1(dev, num_splits):
     assert_attn_close(got, decode_reference(case), what=f"cfg1 splits={num_splits}")
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("B,d", [(1, 128), (3, 128), (7, 64), (32, 128), (64, 128)])
+def test_store_decode_matches_two_calls(dev, fp8, B, d):
+    """nva_store_decode (Attention.forward's decode branch as one call) against
+    store_kvcache + flash_attn_with_kvcache on copies of the same cache: identical
+    output bits and identical cache bits, and the oracle over the stored cache.
+    Batches up to 32 x 8 kv heads take the spread mode, where the store runs
+    inside the decode launch and the holder of key ctx-1 patches the new row into
+    its registers; 64 x 8 takes the balanced mode (store kernel, then decode).
+    Lengths hit a step's first and last row, a page boundary, one key and none."""
+    if fp8 and d != 128:
+        pytest.skip("fp8 decode supports head_dim 128 only (nva_decode refuses it)")
+    from nanovllm_amd import workloads as W
+    m = nva()
+    base = [1, 33, 0, 256, 257, 700, 31, 32, 64, 1023]
+    lengths = [base[i % len(base)] + (i // len(base)) * 5 for i in range(B)]
+    case = W.make_decode_case(B, 16, 8, 0, 0, 8 * B + 2, fp8=fp8, seed=B + 11 * d, head_dim=d, bulk_device=dev,
+                              lengths=lengths, table_width=max(5, -(-max(lengths) // 256)))
+    kc1, vc1 = case.k_cache.clone(), case.v_cache.clone()
+    fused = m.store_and_decode(case.q.unsqueeze(1), case.k_new, case.v_new, kc1, vc1, case.slot_mapping,
+                               case.context_lens, case.block_tables, softmax_scale=case.scale,
+                               k_scale=case.k_scale, v_scale=case.v_scale)
+    m.store_kvcache(case.k_new, case.v_new, case.k_cache, case.v_cache, case.slot_mapping, case.k_scale, case.v_scale)
+    two = m.flash_attn_with_kvcache(case.q.unsqueeze(1), case.k_cache, case.v_cache, case.context_lens,
+                                    case.block_tables, case.scale, True, k_scale=case.k_scale, v_scale=case.v_scale)
+    torch.cuda.synchronize()
+    view = bits8 if fp8 else bits16
+    assert np.array_equal(view(kc1), view(case.k_cache)) and np.array_equal(view(vc1), view(case.v_cache))
+    assert np.array_equal(bits16(fused), bits16(two)), f"B={B} fp8={fp8}: fused output differs from the two calls"
+    tol = dict(max_abs=FP8_MAX_ABS, mean_abs=FP8_MAX_ABS) if fp8 else {}
+    assert_attn_close(f32(fused[:, 0]), decode_reference(case), what=f"store+decode B={B} fp8={fp8} d={d}", **tol)
+
+
 def test_decode_cfg3_full(dev):
     from nanovllm_amd import workloads as W
     case = W.config3(dev)
