@@ -880,7 +880,7 @@ __global__ __launch_bounds__(64 * kMergeHeads) void decode_merge_kernel(DecodePa
 // small-batch step is latency-bound and this kernel's code is fetched cold by
 // each CU, so a 32-way unrolled batch (twice the code) measured slower
 // (captured batch 1: 12.6 vs 13.1 us per layer; batch 16: 22.4 vs 24.0).
-constexpr int kSpreadMergeBatch = 16;
+constexpr int kSpreadMergeBatch = kSpreadMaxShares;  // one batch holds every share
 
 __global__ __launch_bounds__(64) void decode_spread_merge_kernel(DecodeParams p) {
   const int b = blockIdx.x / p.num_heads;
@@ -955,6 +955,7 @@ DecodePlan plan_decode(int32_t batch, int32_t num_kv_heads, int32_t max_blocks, 
   if (requested_splits == 0 && pairs <= kSpreadMaxPairs && max_blocks <= kWgMaxBlocks) {
     int64_t S = kSpreadTargetWaves / pairs;
     if (S > table_steps) S = table_steps;
+    if (S > kSpreadMaxShares) S = kSpreadMaxShares;
     if (S < 1) S = 1;
     plan.pages_per_split = max_blocks;
     plan.num_splits = 1;

@@ -165,15 +165,15 @@ def test_decode_workspace_plan(lib):
     # never more ranges than steps: 2 sequences x 1 page x 8 steps (balanced forced with -1)
     assert f(2, 16, 8, 128, 1, 256, 0, -1) == rnd((2 + 16) * 16 * 130 * 4 + 3 * 4)
     # small batch, table of at most 64 blocks (batch * nkv <= 256): spread mode,
-    # S = min(1024 / (batch * nkv), table steps) shares per sequence, B * S slots
+    # S = min(1024 / (batch * nkv), table steps, 16) shares per sequence, B * S slots
     spread = lambda B, S: rnd(B * S * 16 * 130 * 4)
     assert f(2, 16, 8, 128, 1, 256, 0, 0) == spread(2, 8)      # 8 table steps
     assert f(32, 16, 8, 128, 16, 256, 0, 0) == spread(32, 4)   # 1024 / 256 pairs
     assert f(32, 16, 8, 128, 16, 256, 1, 0) == spread(32, 4)
-    assert f(4, 16, 8, 128, 17, 256, 0, 0) == spread(4, 32)
+    assert f(4, 16, 8, 128, 17, 256, 0, 0) == spread(4, 16)     # at most 16 shares
     assert f(1, 16, 8, 128, 1, 32, 0, 0) == 0                  # one share: written directly
     assert f(33, 16, 8, 128, 16, 256, 0, 0) == rnd((33 + 128) * 16 * 130 * 4 + 34 * 4)  # 264 pairs: balanced
-    assert f(4, 16, 8, 128, 65, 256, 0, 0) > spread(4, 32)     # 65-block table: balanced
+    assert f(4, 16, 8, 128, 65, 256, 0, 0) > spread(4, 16)     # 65-block table: balanced
     # deterministic, and nothing for an empty batch
     assert f(64, 64, 8, 128, 128, 256, 1, 0) == f(64, 64, 8, 128, 128, 256, 1, 0) > 0
     assert f(0, 16, 8, 128, 8, 256, 0, 0) == 0

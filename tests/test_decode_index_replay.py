@@ -247,7 +247,7 @@ def test_balanced_decode_indices_many_shapes(B, lo, hi):
 
 # ---------------------------------------------------------------------------
 # Spread mode (paged_decode_spread_kernel, plan_decode's small-batch branch).
-K_SPREAD_MAX_PAIRS, K_SPREAD_TARGET, K_MAX_BLOCKS = 256, 1024, 64
+K_SPREAD_MAX_PAIRS, K_SPREAD_TARGET, K_MAX_BLOCKS, K_SPREAD_MAX_SHARES = 256, 1024, 64, 16
 
 
 def spread_plan(batch, nkv, max_blocks, block_size):
@@ -255,7 +255,7 @@ def spread_plan(batch, nkv, max_blocks, block_size):
     if pairs > K_SPREAD_MAX_PAIRS or max_blocks > K_MAX_BLOCKS:
         return None
     table_steps = (max_blocks * block_size + 31) // 32
-    return max(1, min(K_SPREAD_TARGET // pairs, table_steps))
+    return max(1, min(K_SPREAD_TARGET // pairs, table_steps, K_SPREAD_MAX_SHARES))
 
 
 def replay_spread(lengths, nh, nkv, D, max_blocks, block_size):
