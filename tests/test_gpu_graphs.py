@@ -129,3 +129,45 @@ def test_batches_beyond_the_graphs_run_eagerly(dev):
     ref = _eager(twins, *batch)
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
+
+
+def test_fp8_cache_replay_matches_oracle(dev):
+    """Captured decode over an fp8 e4m3fn cache (allocated and bound by
+    engine.kv_cache.allocate_kv_cache, scales from amax): every replayed layer
+    matches the oracle on the dequantised cache, and the new token's stored codes
+    equal the oracle's quantisation -- at batches served by the spread mode, where
+    the store runs (and quantises) inside the decode launch, and by the balanced
+    mode (48 sequences x 8 kv heads)."""
+    import nanovllm_amd as nva
+    from nanovllm_amd.engine.decode_graphs import DecodeGraphs
+    from nanovllm_amd.engine.kv_cache import allocate_kv_cache
+    from oracle import attention_oracle as O
+    from _helpers import FP8_MAX_ABS, bits8
+    max_blocks, num_blocks = 4, 200
+    layers = torch.nn.ModuleList([nva.Attention(NH, D, D ** -0.5, NKV) for _ in range(2)])
+    kv = allocate_kv_cache(layers.modules(), 2, BS_PAGE, NKV, D, kv_dtype=torch.float8_e4m3fn,
+                           num_blocks=num_blocks, device=dev)
+    g = torch.Generator(device=dev).manual_seed(21)
+    # Scales first, amax 8 (far beyond any N(0,1) draw of the new tokens, so x / scale stays
+    # under 448 and no NaN code is stored), then random cache codes within range.
+    for i in range(2):
+        kv.set_scales_from_amax(i, torch.full((NKV,), 8.0, device=dev), torch.full((NKV,), 8.0, device=dev))
+        for c, sc in ((kv.kv_cache[0, i], kv.kv_scale[0, i]), (kv.kv_cache[1, i], kv.kv_scale[1, i])):
+            src = torch.randn(num_blocks, BS_PAGE, NKV, D, generator=g, device=dev).clamp_(-7.5, 7.5)
+            c.copy_((src / sc[None, None, :, None]).to(torch.float8_e4m3fn))
+    graphs = DecodeGraphs(list(layers), max_bs=48, max_num_blocks=max_blocks).capture()
+    for i, bs in enumerate([1, 3, 16, 40, 2]):
+        q, k, v, slots, ctx, bt = _batch(dev, bs, max_blocks - 1, num_blocks, seed=300 + i)
+        got = torch.stack(graphs.run(q, k, v, slots, ctx, bt))
+        torch.cuda.synchronize()
+        for li, a in enumerate(layers):
+            ek = O.quantize_e4m3fn(f32(k).reshape(bs, NKV, D), f32(a.k_scale))
+            ev = O.quantize_e4m3fn(f32(v).reshape(bs, NKV, D), f32(a.v_scale))
+            assert np.array_equal(bits8(a.k_cache).reshape(-1, NKV, D)[slots.long().cpu().numpy()], ek)
+            assert np.array_equal(bits8(a.v_cache).reshape(-1, NKV, D)[slots.long().cpu().numpy()], ev)
+            case = SimpleNamespace(batch=bs, context_lens=ctx, block_tables=bt, q=q.view(-1, NH, D),
+                                   num_heads=NH, num_kv_heads=NKV, head_dim=D, block_size=BS_PAGE,
+                                   scale=D ** -0.5, k_cache=a.k_cache, v_cache=a.v_cache, k_scale=a.k_scale,
+                                   v_scale=a.v_scale)
+            assert_attn_close(f32(got[li]).reshape(bs, NH, D), decode_reference(case), max_abs=FP8_MAX_ABS,
+                              mean_abs=FP8_MAX_ABS, what=f"fp8 graph bs={bs} layer {li} vs oracle")
