@@ -400,14 +400,18 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
   // One 32-key step: softmax of the scores s_cur of keys key0 .. key0+31
   // and O^T += V^T P^T with V from `sb_v`; the QK MFMAs of the following step
   // (keys at `sb_next`) are issued in between, so the matrix pipe works on
-  // them while the VALU does the exponentials.  Without a following step they
-  // run on `sb_v` and their result is unused, which keeps the block branch-free.
-  auto step = [&](f32x16& sv, f32x16& s_next, int key0, const char* sb_v, const char* sb_next, bool next) {
+  // them while the VALU does the exponentials.  After the last tile there is
+  // no following step: they still read `sb_next`, the ring stage after the
+  // last tile (no copy writes it then, so the stale read is harmless), and
+  // their result is unused.  Reading it unconditionally keeps the block
+  // branch-free and every operand address a base plus an immediate (choosing
+  // between two stages cost a VALU add per K read: 2.5% at config 4).
+  auto step = [&](f32x16& sv, f32x16& s_next, int key0, const char* sb_v, const char* sb_next) {
     if (key0 < wave_kmax) {  // otherwise every key of this step is masked for this wave
       // K operands of the following QK, read first so that they have landed
       // by the time its MFMAs issue between the exponentials
       bf16x8 kr[NKS];
-      k_read(next ? sb_next : sb_v, kr);
+      k_read(sb_next, kr);
       if (key0 + 32 > wave_full || key0 + 32 > kmax) {
         // score i is key key0 + 4h + c_i (c_i = 8 (i / 4) + i % 4): it stays
         // when c_i <= limit - key0 - 4h, one compare against an immediate each
@@ -512,7 +516,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
   };
   auto tile_iter = [&](int it, const char* cur, const char* nxt, char* fill) {
     const int kb = it * kBK;
-    step(s0, s1, kb, cur, cur + 32 * RB, true);
+    step(s0, s1, kb, cur, cur + 32 * RB);
     if (it + 2 < ntiles)
       wait_vmem<P>();  // tile it+2's copy may stay in flight
     else
@@ -525,7 +529,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
       stg.template copy_part<0, P / 2>(item, fill, src3, it + 3);
       advance();
     }
-    step(s1, s0, kb + 32, cur + 32 * RB, nxt, it + 1 < ntiles);
+    step(s1, s0, kb + 32, cur + 32 * RB, nxt);
     if (it + 3 < ntiles) stg.template copy_part<P / 2, P>(item, fill, src3, it + 3);
   };
 
