@@ -76,11 +76,16 @@ def _pools(case, n):
     return pools
 
 
-def bench_decode(case, steps, warmup, n_pools=2, with_store=True, warm_s=1.0):
+def bench_decode(case, steps, warmup, n_pools=2, with_store=True, warm_s=1.0, fused=False):
+    """A decode step over `steps` rotations of the cache pools.  fused: the step is
+    one store_and_decode call (Attention.forward's decode branch); otherwise
+    store_kvcache then flash_attn_with_kvcache, timed apart."""
     import torch
     import nanovllm_amd as nva
     pools = _pools(case, n_pools)
     q = case.q.unsqueeze(1)
+    if fused:
+        return _bench_decode_fused(case, pools, q, steps, warmup, warm_s)
 
     def store(i):
         kc, vc = pools[i % n_pools]
@@ -120,6 +125,37 @@ def bench_decode(case, steps, warmup, n_pools=2, with_store=True, warm_s=1.0):
                 attn_bytes=attn_bytes, store_bytes=store_bytes,
                 step_gbs=(attn_bytes + store_bytes) / (step_ms * 1e-3) / 1e9,
                 attn_gbs=attn_bytes / (attn_ms * 1e-3) / 1e9)
+
+
+def _bench_decode_fused(case, pools, q, steps, warmup, warm_s):
+    import torch
+    import nanovllm_amd as nva
+    n_pools = len(pools)
+
+    def one(i):
+        kc, vc = pools[i % n_pools]
+        return nva.store_and_decode(q, case.k_new, case.v_new, kc, vc, case.slot_mapping, case.context_lens,
+                                    case.block_tables, case.scale, k_scale=case.k_scale, v_scale=case.v_scale)
+
+    _warm(one, warmup, warm_s)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record()
+        one(i)
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = ev[0][0].elapsed_time(ev[-1][1]) / steps
+    call_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    B = case.batch
+    D = case.num_kv_heads * case.head_dim
+    store_bytes = 2 * B * D * 2 + 2 * B * D * case.k_cache.element_size() + 4 * B
+    attn_bytes = case.kv_bytes()
+    return dict(step_ms=step_ms, call_ms=call_ms, wall_ms=wall * 1e3 / steps, attn_bytes=attn_bytes,
+                store_bytes=store_bytes, step_gbs=(attn_bytes + store_bytes) / (step_ms * 1e-3) / 1e9,
+                call_gbs=(attn_bytes + store_bytes) / (call_ms * 1e-3) / 1e9)
 
 
 def bench_prefill(case, steps, warmup, warm_s=1.0):
@@ -383,6 +419,10 @@ def main(argv=None):
         log(f"[bench] cfg3 step {d3['step_ms']*1e3:.1f} us, attention {d3['attn_ms']*1e3:.1f} us "
             f"= {d3['attn_gbs']:.0f} GB/s, store {d3['store_ms']*1e3:.1f} us")
         out["cfg3"] = d3
+        f3 = bench_decode(c3, steps, warmup, warm_s=args.warm_seconds, fused=True)
+        log(f"[bench] cfg3 fused step {f3['step_ms']*1e3:.1f} us (store_and_decode: the store inside the "
+            f"decode launch), call {f3['call_ms']*1e3:.1f} us")
+        out["cfg3_fused"] = f3
         # the CPU baselines run last, so the GPU workloads follow each other
         # without the GPU idling (and its clocks dropping) for the CPU samples
         if not args.no_cpu:
@@ -390,8 +430,8 @@ def main(argv=None):
         del c3
         log("[bench] config 1: decode step, B=4 (cache-resident: no roofline claim)")
         c1 = W.config1(dev)
-        out["cfg1"] = bench_decode(c1, steps, warmup, n_pools=1, warm_s=args.warm_seconds)
-        log(f"[bench] cfg1 step {out['cfg1']['step_ms']*1e3:.1f} us, attention {out['cfg1']['attn_ms']*1e3:.1f} us")
+        out["cfg1"] = bench_decode(c1, steps, warmup, n_pools=1, warm_s=args.warm_seconds, fused=True)
+        log(f"[bench] cfg1 step {out['cfg1']['step_ms']*1e3:.1f} us (store_and_decode, store fused)")
         if not args.no_cpu:
             host["cfg1"] = c1.to("cpu")
         del c1
@@ -474,15 +514,22 @@ def main(argv=None):
                             "traffic_source": "profiles/decode_hbm_traffic.md",
                             "bytes_per_launch": d3["attn_bytes"], "launch_us": round(d3["attn_ms"] * 1e3, 2)}
         line["store_kvcache_us"] = round(d3["store_ms"] * 1e3, 2)
+        if "cfg3_fused" in out:
+            f3 = out["cfg3_fused"]
+            line["fused_step"] = {"note": "the same step as one store_and_decode call (Attention.forward's decode "
+                                          "branch): the store runs inside the decode launch",
+                                  "step_us": round(f3["step_ms"] * 1e3, 2), "call_us": round(f3["call_ms"] * 1e3, 2),
+                                  "gbs": round(f3["step_gbs"], 1)}
     if "cpu" in out:
         if "cfg3" in out["cpu"]:
             line["cpu_baseline"] = out["cpu"]["cfg3"]
         line["cpu_baselines"] = out["cpu"]
     if "cfg1" in out:
         d1 = out["cfg1"]
-        line["cfg1_decode"] = {"note": "cache-resident (5 MB): reported, no roofline claim",
-                               "step_us": round(d1["step_ms"] * 1e3, 2), "attn_us": round(d1["attn_ms"] * 1e3, 2),
-                               "attn_gbs": round(d1["attn_gbs"], 1), "bytes": d1["attn_bytes"]}
+        line["cfg1_decode"] = {"note": "cache-resident (5 MB): reported, no roofline claim; one store_and_decode "
+                                       "call per step",
+                               "step_us": round(d1["step_ms"] * 1e3, 2), "call_us": round(d1["call_ms"] * 1e3, 2),
+                               "gbs": round(d1["call_gbs"], 1), "bytes": d1["attn_bytes"] + d1["store_bytes"]}
     if "cfg4" in out or "cfg2" in out:
         line["prefill"] = {k: {"tflops": round(out[k]["tflops"], 1), "ms": round(out[k]["ms"], 4),
                                "gflop": round(out[k]["flops"] / 1e9, 2),

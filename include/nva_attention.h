@@ -150,13 +150,15 @@ int nva_decode(const void* q, int64_t q_row_stride,
  * head_dim) bf16 rows at key_row_stride / value_row_stride; slot_mapping: (batch,) int32, slots
  * outside [0, num_blocks*block_size) skipped; every other argument as nva_decode (same workspace,
  * nva_decode_workspace_bytes).  It has no single counterpart in the reference.
- * When nva_decode's plan is the small-batch spread mode, the store runs inside the decode launch:
- * the workgroup that reads key cache_seqlens[b]-1 writes the new rows and uses them from registers.
+ * When nva_decode's plan is the small-batch spread mode, or the balanced mode over a bf16 cache,
+ * the store runs inside the decode launch: the wave that reads key cache_seqlens[b]-1 writes the
+ * new rows and uses them from registers.
  * That equals store-then-decode when slot_mapping[b] is the slot of key cache_seqlens[b]-1 of
  * sequence b (as every decode step the reference runs has it: prepare_decode, model_runner.py
  * :218-229) and no other sequence of the batch reads that slot; otherwise the attention over the
- * new token's slot is unspecified (the store itself is done).  Other plans run the store kernel,
- * then the decode.
+ * new token's slot is unspecified (the store itself is done).  Other plans (fixed splits, an fp8
+ * cache in balanced mode) run the store kernel, then the decode.  The fused paths need fewer than
+ * 2^31 slots in the pool (num_blocks * block_size); larger pools store first.
  */
 int nva_store_decode(const void* key, int64_t key_row_stride,
                      const void* value, int64_t value_row_stride,

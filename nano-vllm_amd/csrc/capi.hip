@@ -363,9 +363,14 @@ int decode_impl(const void* q, int64_t q_row_stride, const void* k_cache, const 
   p.head_dim = head_dim;
   p.scale_log2 = softmax_scale * kLog2e;
   if (store) {
-    // The spread mode stores inside its own launch (16-byte source pieces);
-    // otherwise the store kernel runs first.
-    if (plan.spread > 0 && (kv_dtype == NVA_DTYPE_FP8_E4M3 || store_vec == 16)) {
+    // The spread mode, and the balanced mode over a bf16 cache, store inside
+    // their own launch (16-byte source pieces); otherwise the store kernel
+    // runs first.
+    // (The fused kernels compare slots in 32 bits: pools below 2^31 slots.)
+    const bool bf16_vec = kv_dtype == NVA_DTYPE_BF16 && store_vec == 16;
+    const bool small_pool = num_blocks * block_size < (int64_t{1} << 31);
+    if (small_pool && ((plan.spread > 0 && (kv_dtype == NVA_DTYPE_FP8_E4M3 || store_vec == 16)) ||
+                       (plan.balanced_ranges > 0 && bf16_vec))) {
       p.new_k = static_cast<const uint16_t*>(store->key);
       p.new_v = static_cast<const uint16_t*>(store->value);
       p.new_k_stride = store->key_row_stride;

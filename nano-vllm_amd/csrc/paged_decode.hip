@@ -23,6 +23,8 @@
 // sequence each wave writes (unnormalised O, max, sum) and decode_merge_kernel
 // combines the splits with a log-sum-exp merge.  The split count depends only
 // on host-side sizes, so the launch is graph-capture safe.
+#include <type_traits>
+
 #include "nva_common.h"
 #include "nva_kernels.h"
 
@@ -104,12 +106,17 @@ struct StepRegs<true> {
   u32x2 v[8];
 };
 
+typedef const __attribute__((address_space(4))) int32_t const_i32;
+
 // Per-wave constants of a work item.
 struct WaveItem {
   const char* kbase;      // k_cache + kv head offset (bytes)
   const char* vbase;
   int64_t slot_bytes;     // bytes between consecutive slots
-  const int32_t* bt;      // block table row of the sequence
+  // Block table row of the sequence, read with ordinary loads: through the
+  // constant address space (scalar loads) the balanced decode measured 2 us
+  // slower at config 3.
+  const int32_t* bt;
   int64_t num_blocks;
   int block_size;
   int k_begin;
@@ -170,6 +177,7 @@ __device__ __forceinline__ void load_step(StepRegs<FP8>& r, const WaveItem& w, i
 struct StepRsrc {
   __amdgpu_buffer_rsrc_t k, v;
   int nvalid;
+  int row0;  // cache slot of the step's first key (low 32 bits)
 };
 
 // Records covering rows [0, nvalid) of a step whose row 0 is at `base`.
@@ -188,6 +196,7 @@ __device__ __forceinline__ StepRsrc step_rsrc(const WaveItem& w, int i, int nste
   r.k = rows_rsrc(w.kbase + row0 * w.slot_bytes, nvalid, sb, ROW_BYTES);
   r.v = rows_rsrc(w.vbase + row0 * w.slot_bytes, nvalid, sb, ROW_BYTES);
   r.nvalid = nvalid;
+  r.row0 = static_cast<int>(row0);
   return r;
 }
 
@@ -294,7 +303,7 @@ __device__ __forceinline__ void compute_step(StepRegs<FP8>& r, int nvalid, int g
 // No register patch (every caller but the fused store).
 struct NoPatch {
   template <class R>
-  __device__ __forceinline__ void apply(R&, int) const {}
+  __device__ __forceinline__ void apply(R&, int, int) const {}
 };
 
 // The new token's key and value of one kv head, as this lane holds them in a
@@ -307,8 +316,9 @@ struct NoPatch {
 template <bool FP8, int D>
 struct NewRow {
   static constexpr int NK = D / 32;  // 16-byte bf16 source pieces of the key row per lane
-  int step = -1;
-  int row = 0;
+  int step = -1;     // local step holding the new key (-1: none)
+  int row = 0;       // its row in that step
+  int slot = -1;     // the new token's slot (the pool has fewer than 2^31 slots)
   float ks = 1.f, vs = 1.f;
   u32x4 k[NK];
   u32x4 v;
@@ -326,11 +336,16 @@ struct NewRow {
     v = ld16(vin + 8 * (D == 128 || n < D / 8 ? n : 0));
   }
 
-  // Registers of local step i: the K tile row `row` lives in lanes
-  // n = 4 (row / 8) + row % 4 (tile t = row / 4 % 2), the V row in lanes
-  // g = row / 8 (register row % 8).
-  __device__ __forceinline__ void apply(StepRegs<FP8>& r, int i) const {
-    if (i != step) return;
+  // Registers of local step i, whose first key is at cache slot row0: the
+  // K tile row `row` lives in lanes n = 4 (row / 8) + row % 4 (tile
+  // t = row / 4 % 2), the V row in lanes g = row / 8 (register row % 8).  Only
+  // a step that read the new token's slot is patched (slot_mapping[b] is then
+  // the slot of key ctx-1, as every decode step produces it).
+  __device__ __forceinline__ void apply(StepRegs<FP8>& r, int i, int row0) const {
+    if (i != step || row0 + row != slot) return;
+    // a side effect: the selects below stay behind the branch (if-converted,
+    // they would run on every step of the loop)
+    asm volatile("");
     const int lane = threadIdx.x & 63;
     const int n = lane & 15;
     const int g = lane >> 4;
@@ -421,20 +436,42 @@ __device__ __forceinline__ void segment_accumulate(const DecodeParams& p, int kv
   const int nsteps = (k_end - k_begin + 31) >> 5;
   if (BUF && nsteps > 0) {
     // two steps in flight: step i+1's loads go out before step i is computed,
-    // step i+2's before step i+1 (past the end they return zeros)
+    // step i+2's before step i+1 (past the end they return zeros).  With a
+    // patch (only ever of the last step) the loop stops one step short and the
+    // last step, already loaded into A or B by it, is patched and computed
+    // after it: inside the loop the patch's branch would move the waits for
+    // each step's loads to the step's start.
     constexpr int RB = D * EB;
     StepRegs<FP8> A, B;
     StepRsrc ra = step_rsrc<HOIST, RB>(w, 0, nsteps, bt_row);
     load_step_buf<FP8, D>(A, w, ra);
-    for (int i = 0; i < nsteps; i += 2) {
-      const StepRsrc rb = step_rsrc<HOIST, RB>(w, i + 1, nsteps, bt_row);
-      load_step_buf<FP8, D>(B, w, rb);
-      patch.apply(A, i);
-      compute_step<FP8, D, false>(A, ra.nvalid, g, qop, sl2, acc, m_run, l_run);
-      ra = step_rsrc<HOIST, RB>(w, i + 2, nsteps, bt_row);
-      load_step_buf<FP8, D>(A, w, ra);
-      if (i + 1 < nsteps) {
-        patch.apply(B, i + 1);
+    if constexpr (std::is_same<Patch, NoPatch>::value) {
+      for (int i = 0; i < nsteps; i += 2) {
+        const StepRsrc rb = step_rsrc<HOIST, RB>(w, i + 1, nsteps, bt_row);
+        load_step_buf<FP8, D>(B, w, rb);
+        compute_step<FP8, D, false>(A, ra.nvalid, g, qop, sl2, acc, m_run, l_run);
+        ra = step_rsrc<HOIST, RB>(w, i + 2, nsteps, bt_row);
+        load_step_buf<FP8, D>(A, w, ra);
+        if (i + 1 < nsteps) compute_step<FP8, D, false>(B, rb.nvalid, g, qop, sl2, acc, m_run, l_run);
+      }
+    } else {
+      const int nloop = nsteps - 1;
+      StepRsrc rb = ra;
+      for (int i = 0; i < nloop; i += 2) {
+        rb = step_rsrc<HOIST, RB>(w, i + 1, nsteps, bt_row);
+        load_step_buf<FP8, D>(B, w, rb);
+        compute_step<FP8, D, false>(A, ra.nvalid, g, qop, sl2, acc, m_run, l_run);
+        ra = step_rsrc<HOIST, RB>(w, i + 2, nsteps, bt_row);
+        load_step_buf<FP8, D>(A, w, ra);
+        if (i + 1 < nloop) compute_step<FP8, D, false>(B, rb.nvalid, g, qop, sl2, acc, m_run, l_run);
+      }
+      // step nloop: in A when nloop is even (loaded as step i + 2 of the last
+      // iteration, or before the loop), else in B (step i + 1)
+      if ((nloop & 1) == 0) {
+        patch.apply(A, nloop, ra.row0);
+        compute_step<FP8, D, false>(A, ra.nvalid, g, qop, sl2, acc, m_run, l_run);
+      } else {
+        patch.apply(B, nloop, rb.row0);
         compute_step<FP8, D, false>(B, rb.nvalid, g, qop, sl2, acc, m_run, l_run);
       }
     }
@@ -461,12 +498,24 @@ __device__ __forceinline__ void segment_accumulate(const DecodeParams& p, int kv
   l += shfl_xor(l, 32);
 }
 
+__device__ __forceinline__ int clamped_len(const DecodeParams& p, int b) {
+  const int ctx = p.seqlens[b];
+  const int cap = p.max_blocks * p.block_size;
+  return ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+}
+
 // One wave, one kv head: attention of the head group's queries over keys
 // [k_begin, k_end) of sequence b.  Writes the normalised output when `direct`,
 // otherwise the unnormalised partial (O * v_scale, running max, sum) at `slot`.
-template <bool FP8, bool PREFETCH, int D, bool BUF = false>
+// STORE: the segment holding key ctx-1 also stores the new token's K and V
+// rows of this kv head at slot_mapping[b], after its own steps, and -- when
+// that slot is key ctx-1's (what every decode step produces) -- patches the
+// rows into its registers in place of the stale ones it loaded, so the result
+// equals store-then-decode without waiting for the store (no other segment
+// reads key ctx-1).
+template <bool FP8, bool PREFETCH, int D, bool BUF = false, bool STORE = false>
 __device__ __forceinline__ void decode_segment(const DecodeParams& p, int kvh, int b, int k_begin, int k_end,
-                                               bool direct, int64_t slot) {
+                                               bool direct, int64_t slot, int ctx = 0) {
   const int lane = threadIdx.x & 63;
   const int n = lane & 15;
   const int g = lane >> 4;
@@ -474,7 +523,41 @@ __device__ __forceinline__ void decode_segment(const DecodeParams& p, int kvh, i
   const bool head_ok = n < p.group;
   f32x4 acc[8];
   float m_run, l;
-  segment_accumulate<FP8, PREFETCH, D, false, BUF>(p, kvh, b, k_begin, k_end, acc, m_run, l);
+  if constexpr (STORE) {
+    // ctx: the sequence's (clamped) length; the segment ending at ctx holds
+    // key ctx-1.  slot_mapping[b] is read with a scalar load (constant address
+    // space); it is needed only at the last step and for the store.
+    const bool holder = ctx > 0 && k_end == ctx;
+    if (holder) {
+      NewRow<FP8, D> nr;
+      // lanes 0..D/8-1 store the key row, lanes 32.. the value row, 8 elements each
+      const int j = lane & 31;
+      const bool is_v = lane >= 32;
+      const uint16_t* kin = p.new_k + b * p.new_k_stride + kvh * D;
+      const uint16_t* vin = p.new_v + b * p.new_v_stride + kvh * D;
+      nr.load(kin, vin, n, g, FP8 ? p.k_scale[kvh] : 1.f, FP8 ? p.v_scale[kvh] : 1.f);
+      const u32x4 x = ld16((is_v ? vin : kin) + 8 * (j & (D / 8 - 1)));
+      nr.step = ((ctx - 1) >> 5) - (k_begin >> 5);
+      nr.row = (ctx - 1) & 31;
+      const int64_t nslot = ((const_i32*)p.slot_mapping)[b];
+      // an invalid slot matches no row0 + row, so nothing is patched
+      nr.slot = static_cast<int>(nslot);
+      segment_accumulate<FP8, PREFETCH, D, false, BUF>(p, kvh, b, k_begin, k_end, acc, m_run, l, 0, nr);
+      if (j < D / 8 && nslot >= 0 && nslot < static_cast<int64_t>(p.num_blocks) * p.block_size) {
+        constexpr int EB = FP8 ? 1 : 2;
+        char* dst = static_cast<char*>(const_cast<void*>(is_v ? p.v_cache : p.k_cache)) +
+                    (nslot * p.num_kv_heads + kvh) * D * EB + 8 * j * EB;
+        if constexpr (FP8)
+          *reinterpret_cast<u32x2*>(dst) = bf16x8_to_e4m3fn(x, is_v ? p.v_scale[kvh] : p.k_scale[kvh]);
+        else
+          *reinterpret_cast<u32x4*>(dst) = x;
+      }
+    } else {
+      segment_accumulate<FP8, PREFETCH, D, false, BUF>(p, kvh, b, k_begin, k_end, acc, m_run, l);
+    }
+  } else {
+    segment_accumulate<FP8, PREFETCH, D, false, BUF>(p, kvh, b, k_begin, k_end, acc, m_run, l);
+  }
   const float vscale = FP8 ? p.v_scale[kvh] : 1.0f;
   if (!head_ok || 32 * g >= D) return;  // lanes g >= D/32 hold no output columns
   if (direct) {
@@ -506,12 +589,6 @@ __device__ __forceinline__ void decode_segment(const DecodeParams& p, int kvh, i
       *reinterpret_cast<f32x2*>(p.ws_ml + idx * 2) = ml;
     }
   }
-}
-
-__device__ __forceinline__ int clamped_len(const DecodeParams& p, int b) {
-  const int ctx = p.seqlens[b];
-  const int cap = p.max_blocks * p.block_size;
-  return ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
 }
 
 // Launch shape per cache dtype, chosen by measurement on MI355X (config 3 /
@@ -621,16 +698,15 @@ __global__ __launch_bounds__(64) void paged_decode_spread_kernel(DecodeParams p)
       nr.load(kin, vin, n, g, FP8 ? p.k_scale[kvh] : 1.f, FP8 ? p.v_scale[kvh] : 1.f);
       x = ld16((is_v ? vin : kin) + 8 * (j & (D / 8 - 1)));  // every lane loads (no branch), D/8 of them store
       if (ctx > 0) {
-        const int key = ctx - 1;
-        const int blk = key / p.block_size;
-        const int page = __builtin_amdgcn_readlane(bt_row, blk);
-        if (static_cast<int64_t>(page) * p.block_size + (key - blk * p.block_size) == slot) {
-          nr.step = (key >> 5) - (k_begin >> 5);
-          nr.row = key & 31;
-        }
+        nr.step = ((ctx - 1) >> 5) - (k_begin >> 5);
+        nr.row = (ctx - 1) & 31;
+        nr.slot = static_cast<int>(slot);
       }
     }
-    segment_accumulate<FP8, true, D, true, true>(p, kvh, b, k_begin, k_end, acc, m_run, l, bt_row, nr);
+    if (stores)
+      segment_accumulate<FP8, true, D, true, true>(p, kvh, b, k_begin, k_end, acc, m_run, l, bt_row, nr);
+    else
+      segment_accumulate<FP8, true, D, true, true>(p, kvh, b, k_begin, k_end, acc, m_run, l, bt_row);
     if (stores && j < D / 8) {
       constexpr int EB = FP8 ? 1 : 2;
       char* dst = static_cast<char*>(const_cast<void*>(is_v ? p.v_cache : p.k_cache)) +
@@ -730,11 +806,36 @@ __device__ __forceinline__ int64_t used_ranges(int64_t P, int64_t T) {
   return cap < 1 ? 1 : (P < cap ? P : cap);
 }
 
-template <bool FP8, int WAVES, bool PREFETCH, int D>
+// The new token's K and V rows of (b, kvh) written by one thread: a sequence
+// with no context has no step, so no segment holder stores them.
+template <bool FP8, int D>
+__device__ void store_new_rows_thread(const DecodeParams& p, int b, int kvh, int64_t slot) {
+  constexpr int EB = FP8 ? 1 : 2;
+#pragma unroll 1
+  for (int which = 0; which < 2; ++which) {
+    const uint16_t* src = (which ? p.new_v + b * p.new_v_stride : p.new_k + b * p.new_k_stride) + kvh * D;
+    char* dst = static_cast<char*>(const_cast<void*>(which ? p.v_cache : p.k_cache)) +
+                (slot * p.num_kv_heads + kvh) * D * EB;
+    const float sc = FP8 ? (which ? p.v_scale[kvh] : p.k_scale[kvh]) : 1.f;
+#pragma unroll 1
+    for (int j = 0; j < D / 8; ++j) {
+      const u32x4 x = ld16(src + 8 * j);
+      if constexpr (FP8)
+        *reinterpret_cast<u32x2*>(dst + 8 * j) = bf16x8_to_e4m3fn(x, sc);
+      else
+        *reinterpret_cast<u32x4*>(dst + 16 * j) = x;
+    }
+  }
+}
+
+template <bool FP8, int WAVES, bool PREFETCH, int D, bool STORE = false>
 __global__ __launch_bounds__(64 * WAVES) void paged_decode_balanced_kernel(DecodeParams p) {
   constexpr int CH = 64 * WAVES;  // sequences per scan chunk
   __shared__ int s_wsum[WAVES];
-  __shared__ int s_seg[3 * CH];   // (b, first step, end step) of the chunk's pieces
+  // (b, first step, end step) of the chunk's pieces.  (Carrying each
+  // sequence's length here too, instead of re-reading it per segment, measured
+  // 2 us slower at config 3.)
+  __shared__ int s_seg[3 * CH];
   const int tid = threadIdx.x;
   // wave-uniform (readfirstlane): the step buffer resources stay in scalar registers
   const int kvh = __builtin_amdgcn_readfirstlane(blockIdx.y * WAVES + (tid >> 6));
@@ -751,6 +852,17 @@ __global__ __launch_bounds__(64 * WAVES) void paged_decode_balanced_kernel(Decod
     const int incl = block_scan_incl<WAVES>(st, s_wsum, tot);
     if (write_prefix && b < B) p.ws_prefix[b] = T + incl - st;
     T += tot;
+    if constexpr (STORE) {
+      // range 0 of each kv-head group stores the rows of sequences with no context
+      if (blockIdx.x == 0 && b < B && st == 0) {
+        const int64_t slot = p.slot_mapping[b];
+        if (slot >= 0 && slot < static_cast<int64_t>(p.num_blocks) * p.block_size)
+#pragma unroll 1
+          for (int w = 0; w < WAVES; ++w)
+            if (static_cast<int>(blockIdx.y) * WAVES + w < p.num_kv_heads)
+              store_new_rows_thread<FP8, D>(p, b, static_cast<int>(blockIdx.y) * WAVES + w, slot);
+      }
+    }
   }
   if (write_prefix && tid == 0) p.ws_prefix[B] = T;
   const int64_t P = used_ranges(p.balanced_ranges, T);
@@ -784,8 +896,8 @@ __global__ __launch_bounds__(64 * WAVES) void paged_decode_balanced_kernel(Decod
         const int hi = __builtin_amdgcn_readfirstlane(s_seg[3 * i + 2]);
         const int len = __builtin_amdgcn_readfirstlane(clamped_len(p, sb));
         const bool whole = lo == 0 && hi == ((len + 31) >> 5);
-        decode_segment<FP8, PREFETCH, D, DecodeShape<FP8>::kBuf>(p, kvh, sb, 32 * lo, min(32 * hi, len), whole,
-                                                                 static_cast<int64_t>(sb) + r);
+        decode_segment<FP8, PREFETCH, D, DecodeShape<FP8>::kBuf, STORE>(p, kvh, sb, 32 * lo, min(32 * hi, len),
+                                                                        whole, static_cast<int64_t>(sb) + r, len);
       }
     }
     __syncthreads();  // s_seg is rewritten by the next chunk
@@ -991,20 +1103,22 @@ DecodePlan plan_decode(int32_t batch, int32_t num_kv_heads, int32_t max_blocks, 
   return plan;
 }
 
+#define NVA_COMMA ,
 template <bool FP8, int D>
 static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
   constexpr bool PF = DecodeShape<FP8>::kPrefetch;
   const int w = decode_waves_per_group(p.num_kv_heads, FP8 ? 1 : 0);
   const unsigned groups = static_cast<unsigned>((p.num_kv_heads + w - 1) / w);
   constexpr int WMAX = DecodeShape<FP8>::kWaves;  // wider shapes are never launched for this dtype
-#define NVA_LAUNCH_W(KERNEL, GRID)                                                                      \
+// EXTRA: further template arguments (", true" or nothing)
+#define NVA_LAUNCH_W(KERNEL, GRID, EXTRA)                                                               \
   if (w >= 8 && WMAX >= 8)                                                                              \
-    hipLaunchKernelGGL((KERNEL<FP8, (WMAX >= 8 ? 8 : 1), PF, D>), GRID, dim3(64 * (WMAX >= 8 ? 8 : 1)), 0, \
-                       stream, p);                                                                      \
+    hipLaunchKernelGGL((KERNEL<FP8, (WMAX >= 8 ? 8 : 1), PF, D EXTRA>), GRID, dim3(64 * (WMAX >= 8 ? 8 : 1)), \
+                       0, stream, p);                                                                   \
   else if (w >= 4)                                                                                      \
-    hipLaunchKernelGGL((KERNEL<FP8, 4, PF, D>), GRID, dim3(256), 0, stream, p);                         \
+    hipLaunchKernelGGL((KERNEL<FP8, 4, PF, D EXTRA>), GRID, dim3(256), 0, stream, p);                   \
   else                                                                                                  \
-    hipLaunchKernelGGL((KERNEL<FP8, 1, PF, D>), GRID, dim3(64), 0, stream, p);
+    hipLaunchKernelGGL((KERNEL<FP8, 1, PF, D EXTRA>), GRID, dim3(64), 0, stream, p);
   bool merge;
   if (p.spread > 0) {
     const dim3 grid(static_cast<unsigned>(p.spread), static_cast<unsigned>(p.num_kv_heads),
@@ -1020,14 +1134,26 @@ static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
     return hipGetLastError();
   } else if (p.balanced_ranges > 0) {
     const dim3 grid(static_cast<unsigned>(p.balanced_ranges), groups);
-    NVA_LAUNCH_W(paged_decode_balanced_kernel, grid);
+    // The store is fused for a bf16 cache only: its buffer-step loop takes the
+    // patch (an fp8 cache stores first, a few microseconds).
+    bool fused = false;
+    if constexpr (!FP8) {
+      if (p.new_k) {
+        NVA_LAUNCH_W(paged_decode_balanced_kernel, grid, NVA_COMMA true);
+        fused = true;
+      }
+    }
+    if (!fused) {
+      NVA_LAUNCH_W(paged_decode_balanced_kernel, grid, );
+    }
     merge = true;
   } else {
     const dim3 grid(groups, p.num_splits, p.batch);
-    NVA_LAUNCH_W(paged_decode_split_kernel, grid);
+    NVA_LAUNCH_W(paged_decode_split_kernel, grid, );
     merge = p.num_splits > 1;
   }
 #undef NVA_LAUNCH_W
+#undef NVA_COMMA
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !merge) return e;
   const dim3 mgrid(static_cast<unsigned>(p.batch * ((p.num_heads + kMergeHeads - 1) / kMergeHeads)));

@@ -235,9 +235,10 @@ def store_and_decode(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, k_
                      k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None) -> torch.Tensor:
     """The decode branch of Attention.forward as one call: store_kvcache of the new
     rows (attention.py:32-39), then flash_attn_with_kvcache (attention.py:75-77).
-    Small batches run the store inside the decode launch (nva_store_decode); the
-    result equals the two calls when slot_mapping[b] is the slot of key
-    cache_seqlens[b]-1, as prepare_decode (model_runner.py:218-229) produces it."""
+    The spread mode (small batches) and the balanced mode over a bf16 cache run the
+    store inside the decode launch (nva_store_decode); the result equals the two
+    calls when slot_mapping[b] is the slot of key cache_seqlens[b]-1, as
+    prepare_decode (model_runner.py:218-229) produces it."""
     N = key.shape[0]
     if N != q.shape[0]:
         raise RuntimeError("one new key/value row per sequence")

@@ -147,23 +147,31 @@ def test_decode_cfg1(dev, num_splits):
 
 
 @pytest.mark.parametrize("fp8", [False, True])
-@pytest.mark.parametrize("B,d", [(1, 128), (3, 128), (7, 64), (32, 128), (64, 128)])
-def test_store_decode_matches_two_calls(dev, fp8, B, d):
+@pytest.mark.parametrize("B,d,nh,nkv", [(1, 128, 16, 8), (3, 128, 16, 8), (7, 64, 16, 8), (32, 128, 16, 8),
+                                        (64, 128, 16, 8), (64, 64, 16, 8), (256, 128, 16, 8), (160, 64, 14, 2)])
+def test_store_decode_matches_two_calls(dev, fp8, B, d, nh, nkv):
     """nva_store_decode (Attention.forward's decode branch as one call) against
     store_kvcache + flash_attn_with_kvcache on copies of the same cache: identical
     output bits and identical cache bits, and the oracle over the stored cache.
-    Batches up to 32 x 8 kv heads take the spread mode, where the store runs
-    inside the decode launch and the holder of key ctx-1 patches the new row into
-    its registers; 64 x 8 takes the balanced mode (store kernel, then decode).
-    Lengths hit a step's first and last row, a page boundary, one key and none."""
+    Batches up to 32 x 8 kv heads take the spread mode and larger ones the
+    balanced mode (160 x 2 on one-wave workgroups); both store inside the decode
+    launch, where the holder of key ctx-1 patches the new row into its registers
+    (the balanced mode over an fp8 cache runs the store kernel first).  Lengths
+    hit a step's first and last row, a page boundary, one key and none; a
+    sequence with no context but a valid slot (row 2) is stored all the same."""
     if fp8 and d != 128:
         pytest.skip("fp8 decode supports head_dim 128 only (nva_decode refuses it)")
     from nanovllm_amd import workloads as W
     m = nva()
     base = [1, 33, 0, 256, 257, 700, 31, 32, 64, 1023]
     lengths = [base[i % len(base)] + (i // len(base)) * 5 for i in range(B)]
-    case = W.make_decode_case(B, 16, 8, 0, 0, 8 * B + 2, fp8=fp8, seed=B + 11 * d, head_dim=d, bulk_device=dev,
+    case = W.make_decode_case(B, nh, nkv, 0, 0, 8 * B + 2, fp8=fp8, seed=B + 11 * d, head_dim=d, bulk_device=dev,
                               lengths=lengths, table_width=max(5, -(-max(lengths) // 256)))
+    if B > 2 and lengths[2] == 0:
+        # a page no sequence reads, for the empty sequence's new row
+        used = {int(case.block_tables[b, j]) for b in range(B) for j in range(-(-lengths[b] // 256))}
+        free = min(set(range(8 * B + 2)) - used)
+        case.slot_mapping[2] = free * 256 + 7
     kc1, vc1 = case.k_cache.clone(), case.v_cache.clone()
     fused = m.store_and_decode(case.q.unsqueeze(1), case.k_new, case.v_new, kc1, vc1, case.slot_mapping,
                                case.context_lens, case.block_tables, softmax_scale=case.scale,
