@@ -913,12 +913,20 @@ __global__ __launch_bounds__(64 * WAVES) void paged_decode_balanced_kernel(Decod
 // One pass: the loads of up to eight partials are issued together and folded
 // into a running (max, sum, output) online, so the only dependent load before
 // them is the step prefix.
-constexpr int kMergeHeads = 4;  // heads (waves) per merge workgroup
+// WIDE (plans with many partials per sequence): one workgroup per (sequence,
+// head) instead; its four waves fold a quarter of the partials each and wave 0
+// combines their states through LDS, so a long list costs a quarter of the
+// dependent load batches (a one-kv-head fp8 decode at B=64, 32 ranges per
+// sequence: 16.7 us as one wave per head).
+constexpr int kMergeHeads = 4;    // heads (waves) per merge workgroup
+constexpr int kMergeWideMin = 8;  // ranges per sequence (on average) from which the merge is WIDE
 
+template <bool WIDE>
 __global__ __launch_bounds__(64 * kMergeHeads) void decode_merge_kernel(DecodeParams p) {
   const int hgroups = (p.num_heads + kMergeHeads - 1) / kMergeHeads;
-  const int b = blockIdx.x / hgroups;
-  const int h = (blockIdx.x - b * hgroups) * kMergeHeads + (threadIdx.x >> 6);
+  const int b = WIDE ? blockIdx.x / p.num_heads : blockIdx.x / hgroups;
+  const int wq = threadIdx.x >> 6;  // WIDE: the wave's quarter of the partials
+  const int h = WIDE ? static_cast<int>(blockIdx.x) - b * p.num_heads : (blockIdx.x - b * hgroups) * kMergeHeads + wq;
   const int lane = threadIdx.x & 63;
   int64_t first, count;
   bool zero = false;
@@ -952,13 +960,15 @@ __global__ __launch_bounds__(64 * kMergeHeads) void decode_merge_kernel(DecodePa
   };
   const bool cols = 2 * lane < p.head_dim;  // lane owns output columns 2 lane, 2 lane + 1
   float M = kNegInf, L = 0.f, o0 = 0.f, o1 = 0.f;
+  const int64_t s_lo = WIDE ? count * wq / kMergeHeads : 0;
+  const int64_t s_hi = WIDE ? count * (wq + 1) / kMergeHeads : count;
   if (!zero) {
-    for (int64_t s0 = 0; s0 < count; s0 += 8) {
+    for (int64_t s0 = s_lo; s0 < s_hi; s0 += 8) {
       f32x2 ml[8], v[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int64_t s = s0 + u;
-        const bool ok = s < count && has_data(s);
+        const bool ok = s < s_hi && has_data(s);
         const int64_t idx = (first + (ok ? s : 0)) * p.num_heads + h;
         ml[u] = ok ? *reinterpret_cast<const f32x2*>(p.ws_ml + idx * 2) : f32x2{kNegInf, 0.f};
         v[u] = ok && cols ? *reinterpret_cast<const f32x2*>(p.ws_o + idx * p.head_dim + 2 * lane) : f32x2{0.f, 0.f};
@@ -974,6 +984,32 @@ __global__ __launch_bounds__(64 * kMergeHeads) void decode_merge_kernel(DecodePa
         o1 = o1 * a + w * v[u][1];
         M = m_new;
       }
+    }
+  }
+  if constexpr (WIDE) {
+    __shared__ float s_m[kMergeHeads], s_l[kMergeHeads];
+    __shared__ f32x2 s_o[kMergeHeads][64];
+    if (lane == 0) {
+      s_m[wq] = M;
+      s_l[wq] = L;
+    }
+    s_o[wq][lane] = f32x2{o0, o1};
+    __syncthreads();
+    if (wq != 0) return;
+    M = kNegInf;
+    L = o0 = o1 = 0.f;
+#pragma unroll
+    for (int q = 0; q < kMergeHeads; ++q) {
+      const float mq = s_m[q];
+      if (mq == kNegInf) continue;  // a quarter with no partial holding keys
+      const float m_new = fmaxf(M, mq);
+      const float a = fast_exp2(M - m_new);
+      const float w = fast_exp2(mq - m_new);
+      const f32x2 oq = s_o[q][lane];
+      L = L * a + w * s_l[q];
+      o0 = o0 * a + w * oq[0];
+      o1 = o1 * a + w * oq[1];
+      M = m_new;
     }
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -1156,8 +1192,14 @@ static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
 #undef NVA_COMMA
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !merge) return e;
-  const dim3 mgrid(static_cast<unsigned>(p.batch * ((p.num_heads + kMergeHeads - 1) / kMergeHeads)));
-  hipLaunchKernelGGL(decode_merge_kernel, mgrid, dim3(64 * kMergeHeads), 0, stream, p);
+  const int64_t per_seq = p.balanced_ranges > 0 ? p.balanced_ranges / p.batch : p.num_splits;
+  if (per_seq >= kMergeWideMin) {
+    hipLaunchKernelGGL(decode_merge_kernel<true>, dim3(static_cast<unsigned>(p.batch * p.num_heads)),
+                       dim3(64 * kMergeHeads), 0, stream, p);
+  } else {
+    const dim3 mgrid(static_cast<unsigned>(p.batch * ((p.num_heads + kMergeHeads - 1) / kMergeHeads)));
+    hipLaunchKernelGGL(decode_merge_kernel<false>, mgrid, dim3(64 * kMergeHeads), 0, stream, p);
+  }
   return hipGetLastError();
 }
 

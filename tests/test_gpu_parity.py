@@ -138,6 +138,28 @@ def _run_decode(case, num_splits=0, store=True):
     return f32(o[:, 0])
 
 
+@pytest.mark.parametrize("shape", ["long_small_batch", "one_kv_head_fp8", "fixed_12_splits"])
+def test_decode_wide_merge(dev, shape):
+    """Plans with at least 8 partials per sequence on average take the wide merge (four
+    waves per (sequence, head), states combined through LDS): 8 sequences of 15k-20k keys
+    (balanced, 16 ranges each); 64 sequences over one kv head of an fp8 cache (the
+    TP8 share of config 5: 32 ranges each); fixed 12-way splits with a length of 0 and
+    one of 1.  Every sequence against the oracle."""
+    from nanovllm_amd import workloads as W
+    if shape == "long_small_batch":
+        case = W.make_decode_case(8, 16, 8, 15000, 20000, 700, seed=91, bulk_device=dev)
+        ns, tol = 0, {}
+    elif shape == "one_kv_head_fp8":
+        case = W.make_decode_case(64, 8, 1, 17000, 20000, 5100, fp8=True, seed=92, bulk_device=dev)
+        ns, tol = 0, dict(max_abs=FP8_MAX_ABS, mean_abs=FP8_MAX_ABS)
+    else:
+        case = W.make_decode_case(5, 16, 8, 0, 0, 200, seed=93, bulk_device=dev, lengths=[3000, 0, 1, 2500, 7000])
+        ns, tol = 12, {}
+    got = _run_decode(case, ns)
+    for b in range(case.batch):
+        assert_attn_close(got[b:b + 1], decode_reference(case, [b]), what=f"{shape} seq {b}", **tol)
+
+
 @pytest.mark.parametrize("num_splits", [0, -1, 1, 2, 3])
 def test_decode_cfg1(dev, num_splits):
     from nanovllm_amd import workloads as W
