@@ -456,7 +456,7 @@ def test_prefill_pages_outside_the_pool_are_safe(dev):
         assert_attn_close(got[rows_of(case, [s])], prefill_reference(case, [s]), what=f"seq {s}")
 
 
-@pytest.mark.parametrize("nh,nkv", [(16, 16), (16, 8), (32, 8), (64, 8), (14, 2)])
+@pytest.mark.parametrize("nh,nkv", [(16, 16), (16, 8), (32, 8), (64, 8), (14, 2), (64, 4)])
 def test_prefill_shapes(dev, nh, nkv):
     from nanovllm_amd import workloads as W
     lens = [1, 63, 64, 65, 128, 129, 300, 0, 17]
@@ -474,6 +474,39 @@ def test_prefill_prefix_shapes(dev, prefix, shared):
                                shared_prefix=shared)
     got = _run_prefill(case)
     assert_attn_close(got, prefill_reference(case), what=f"prefix={prefix} shared={shared}")
+
+
+@pytest.mark.parametrize("nh,nkv", [(16, 8), (64, 4)])
+def test_prefill_one_new_token_after_long_prefix(dev, nh, nkv):
+    """A prefix-cache hit that leaves a single token to compute (whole pages are cached,
+    block_manager.py:60-82, so a prompt of 16 full pages plus one token prefills 1 query
+    over 4097 keys), next to a fresh 300-token sequence and a 1-token suffix after one
+    cached page; heads 16/8 and 64/4 (Qwen3-235B-A22B's GQA group 16: 16 positions per
+    work item).  Every row against the oracle."""
+    from nanovllm_amd import workloads as W
+    lens, pre = [1, 300, 1], [4096, 0, 256]
+    pages = sum(-(-(q + x) // 256) for q, x in zip(lens, pre)) + 4
+    case = W.make_prefill_case(lens, nh, nkv, pages, prefix_len=pre, seed=4097 + nh, bulk_device=dev,
+                               shared_prefix=False)
+    assert case.block_tables is not None
+    got = _run_prefill(case)
+    assert_attn_close(got, prefill_reference(case), what=f"one new token after a long prefix nh={nh} nkv={nkv}")
+
+
+@pytest.mark.parametrize("prefix", [0, 256])
+def test_prefill_group_16_prefix(dev, prefix):
+    """GQA group 16 (heads 64/4) through the persistent grid, packed and prefix-cached:
+    40 ragged sequences, every row against the oracle."""
+    from nanovllm_amd import workloads as W
+    gen = torch.Generator().manual_seed(1600 + prefix)
+    lens = torch.randint(0, 200, (40,), generator=gen).tolist()
+    lens[7] = 700
+    pages = sum(-(-(prefix + x) // 256) for x in lens) + 4
+    case = W.make_prefill_case(lens, 64, 4, pages, prefix_len=prefix, seed=1601 + prefix, bulk_device=dev,
+                               shared_prefix=False)
+    assert 40 * 4 * -(-700 // 16) > 2 * 256  # the persistent grid serves this call
+    got = _run_prefill(case)
+    assert_attn_close(got, prefill_reference(case), what=f"group 16 prefix={prefix}")
 
 
 SPIKE_POSITIONS = (5, 37, 70, 100, 131, 250)  # spread over both lane halves and several steps
