@@ -27,6 +27,15 @@ the RMS of a normalised row = 1 (unit weight), RMSNorm of a constant row, and
 torch.nn.functional.rms_norm / torch float32 ops on the same inputs; planted
 mistakes (halves swapped, sin sign flipped, mean over the wrong axis, missing
 eps) fail them.
+
+Not pinned: the reference runs both functions under @torch.compile
+(layernorm.py:17, rotary_embedding.py:39), and this module follows the eager
+op sequence.  Inductor may fuse the rotation's products and sums (fused
+multiply-adds round once where eager rounds twice in float32) and may keep
+an intermediate in float32 where eager rounds it to bf16.  The compiled
+reference's bits can therefore differ from this restatement by a bf16 ulp in
+rare elements; no check here (torch is eager, flash-attn and the compiled
+graph are absent) fixes which.
 """
 from __future__ import annotations
 
