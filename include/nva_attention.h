@@ -89,12 +89,15 @@ int nva_store_kvcache(const void* key, int64_t key_row_stride,
  * keys sees keys j <= i + (Lk - Lq).  A query row with no visible key yields zeros.
  * max_seqlen_q bounds the launch grid (host value, graph-capture safe).
  * head_dim 64 or 128; a paged cache needs block_size % 64 == 0 and bf16.
- * workspace: NULL, or nva_prefill_workspace_bytes() bytes, 256-byte aligned, holding
- *   zeros before its first use.  With it, a prefill over many work items hands them out
- *   dynamically (a work queue per XCD); every completed call leaves the workspace zero
- *   again, so it is allocated and cleared once and reused.  Calls that may run at the
- *   same time (different streams) need different workspaces.  NULL selects a static
- *   item order; the results are bit-identical either way.
+ * workspace: NULL, or nva_prefill_workspace_bytes() bytes (about 8.7 MB), 256-byte aligned,
+ *   holding zeros before its first use.  With it, a prefill over many work items hands
+ *   them out dynamically (a work queue per XCD), and a prefill over few items (at most two
+ *   per CU) of packed k/v runs its longest items as two halves of their key range, merged
+ *   in the launch through float32 partials kept in the workspace.  Every completed call
+ *   leaves the workspace's control words zero again, so it is allocated and cleared once
+ *   and reused.  Calls that may run at the same time (different streams) need different
+ *   workspaces.  NULL selects a static item order and whole items: bit-identical to the
+ *   work queue, and within float32 rounding of the halves (the merge reassociates sums).
  */
 int nva_prefill(const void* q, int64_t q_row_stride,
                 const void* k, int64_t k_row_stride,

@@ -139,7 +139,6 @@ int nva_prefill(const void* q, int64_t q_row_stride, const void* k, int64_t k_ro
                 int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads, int32_t num_kv_heads,
                 int32_t head_dim, float softmax_scale, void* out, int64_t out_row_stride, void* workspace,
                 int64_t workspace_bytes, void* stream) {
-  (void)max_seqlen_k;
   if (head_dim != 128 && head_dim != 64)
     return fail(NVA_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", head_dim);
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
@@ -204,7 +203,12 @@ int nva_prefill(const void* q, int64_t q_row_stride, const void* k, int64_t k_ro
   p.head_dim = head_dim;
   p.scale_log2 = softmax_scale * kLog2e;
   p.queue = static_cast<uint32_t*>(workspace);
-  return hip_status(nva::launch_prefill(p, max_seqlen_q, static_cast<hipStream_t>(stream)), "prefill launch");
+  if (workspace) {
+    p.split_ctl = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + nva::kPrefillSplitCtlOffset);
+    p.split_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + nva::kPrefillSplitPartOffset);
+  }
+  return hip_status(nva::launch_prefill(p, max_seqlen_q, max_seqlen_k, static_cast<hipStream_t>(stream)),
+                    "prefill launch");
 }
 
 int64_t nva_prefill_workspace_bytes(void) { return nva::kPrefillWorkspaceBytes; }

@@ -86,6 +86,16 @@ struct PrefillParams {
   int32_t head_dim;           // 64 or 128
   float scale_log2;
   uint32_t* queue;            // null: static item order; else kPrefillQueueWords zeroed words
+  // Key halving of the direct grid (packed k/v): items of at least split_tiles
+  // key tiles (0: off) run as two workgroups over the two halves of their key
+  // tiles, merged by the one that finishes second.  At most split_slots such
+  // items; each has two zeroed control words in split_ctl and
+  // kPrefillSplitPartFloats floats of partial results in split_part.
+  int32_t split_tiles;
+  int32_t split_slots;
+  int32_t split_cus;          // compute units: with the real items, they cap the split items
+  uint32_t* split_ctl;
+  float* split_part;
 };
 
 struct QKNormRopeParams {
@@ -129,17 +139,26 @@ hipError_t launch_store_kvcache(const StoreParams& p, int vec_bytes, hipStream_t
 hipError_t launch_gather_kv(const GatherParams& p, int max_seqlen_k, int kv_dtype, hipStream_t stream);
 hipError_t launch_qk_norm_rope(const QKNormRopeParams& p, hipStream_t stream);
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, hipStream_t stream);
-hipError_t launch_prefill(const PrefillParams& p, int max_seqlen_q, hipStream_t stream);
+hipError_t launch_prefill(const PrefillParams& p, int max_seqlen_q, int max_seqlen_k, hipStream_t stream);
 int prefill_positions_per_tile(int group);  // query positions one prefill workgroup covers
 constexpr int kPrefillMaxGroup = 256;        // rows per prefill workgroup bound the GQA group
 // Work queue of the persistent prefill grid: one claim counter per XCD lane,
 // then the count of finished workgroups.  Zero on entry, zero again on exit.
 constexpr int kPrefillQueueLanes = 8;
 constexpr int kPrefillQueueWords = kPrefillQueueLanes + 1;
-constexpr int64_t kPrefillWorkspaceBytes = 256;
+// Key-halved items of the direct grid: the control words (a finish count and a
+// ready flag per slot, zero on entry and on exit) at byte kPrefillSplitCtlOffset,
+// then one partial per slot from kPrefillSplitPartOffset: O (256 rows x up to
+// 128 head dims, float32, unnormalised) and each row's maximum and sum.
+constexpr int kPrefillSplitSlots = 64;
+constexpr int64_t kPrefillSplitPartFloats = 256 * 128 + 2 * 512;
+constexpr int64_t kPrefillSplitCtlOffset = 256;
+constexpr int64_t kPrefillSplitPartOffset = 1024;
+constexpr int64_t kPrefillWorkspaceBytes = kPrefillSplitPartOffset + kPrefillSplitSlots * kPrefillSplitPartFloats * 4;
+static_assert(kPrefillSplitCtlOffset + 8 * kPrefillSplitSlots <= kPrefillSplitPartOffset, "control words fit");
 // Static device scratch of nva_decode_noalloc (bytes, per GPU).
 constexpr int64_t kDecodeScratchBytes = int64_t{32} << 20;
-static_assert(kPrefillQueueWords * 4 <= kPrefillWorkspaceBytes, "queue fits the workspace");
+static_assert(kPrefillQueueWords * 4 <= kPrefillSplitCtlOffset, "queue fits the workspace");
 
 // Split-K plan shared by nva_decode and nva_decode_workspace_bytes.
 // balanced_ranges > 0: balanced mode with that many step ranges; otherwise

@@ -199,6 +199,7 @@ struct ItemDesc {
   int i0;      // first query position of the tile
   int kmax;    // keys [0, kmax) are visible to some row of the tile
   int ntiles;  // 64-key tiles spanning [0, kmax)
+  int split_slot;  // >= 0: one key half of a split item (workspace slot); -1: a whole item
   bool valid;  // false: no item (s < 0) or a tile past the sequence's end
 };
 
@@ -209,6 +210,7 @@ __device__ __forceinline__ ItemDesc item_desc(const PrefillParams& p, const int*
   d.s = s;
   d.kvh = kvh;
   d.tile = tile;
+  d.split_slot = -1;
   d.valid = false;
   if (s < 0) return d;
   d.q_start = __builtin_amdgcn_readfirstlane(cu_q[s]);
@@ -221,6 +223,203 @@ __device__ __forceinline__ ItemDesc item_desc(const PrefillParams& p, const int*
   d.kmax = max(0, min(d.Lk, last_pos + (d.Lk - d.Lq) + 1));
   d.ntiles = (d.kmax + kBK - 1) / kBK;
   return d;
+}
+
+// Work item of cell c of the direct grid under key halving.  When the cap
+// below is 0 (the launch is oversubscribed, so nothing splits) the cells are
+// those of the plain grid -- x = (sequence, kv head), y = query tile from the
+// last -- flattened.  Otherwise the grid is compact: c = num_kv_heads *
+// position + kv head, over the (sequence, query tile) pairs in level order --
+// query tile descending, then sequence: the heaviest tiles first -- where a
+// split pair takes two consecutive positions, its key halves.  A pair splits
+// when its tile sees at least split_tiles key tiles (keys [0, min(Lk,
+// (t + 1) BP + Lk - Lq))) and fewer such pairs precede it in this order than
+// the cap: split_slots / num_kv_heads, and the CUs the real items leave free
+// (split_cus + split_cus / kSplitSpareDiv - items, over num_kv_heads): a half
+// beyond those waits for a CU, and an oversubscribed launch has no idle CU
+// for it to fill.  Its slots are rank * num_kv_heads + kv head.
+// Every workgroup derives it from cu_seqlens with ballots over 64 sequences at
+// a time, so the result is wave-uniform; s = -1 past the last pair.  (The
+// scan over the levels costs the lighter items time that an oversubscribed
+// launch would put on its critical path, hence the plain cells there.)
+constexpr int kSplitSpareDiv = 8;  // halves may exceed the free CUs by split_cus / kSplitSpareDiv
+
+struct CellItem {
+  int s, kvh, t, half;
+  int pair;  // rank of a split pair, -1 for a whole item
+};
+
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
+}
+
+__device__ __forceinline__ CellItem compact_cell(const PrefillParams& p, int c) {
+  const int lane = threadIdx.x & 63;
+  CellItem ci;
+  ci.s = -1;
+  ci.kvh = 0;
+  ci.t = 0;
+  ci.half = 0;
+  ci.pair = -1;
+  const int BP = p.positions_per_tile;
+  const int thr = (p.split_tiles - 1) * kBK;
+  int pos = 0;    // positions before this level and chunk
+  int cands = 0;  // split candidates before them
+  // the first 64 sequences' lengths stay in registers across the levels
+  int lq0 = 0, lk0 = 0;
+  if (lane < p.num_seqs) {
+    lq0 = p.cu_q[lane + 1] - p.cu_q[lane];
+    lk0 = p.cu_k[lane + 1] - p.cu_k[lane];
+  }
+  // real items: num_kv_heads * the sequences' query tiles
+  int ntq = lq0 > 0 ? (lq0 + BP - 1) / BP : 0;
+  for (int c0 = 64; c0 < p.num_seqs; c0 += 64) {
+    const int sq = c0 + lane;
+    const int lq = sq < p.num_seqs ? p.cu_q[sq + 1] - p.cu_q[sq] : 0;
+    ntq += lq > 0 ? (lq + BP - 1) / BP : 0;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ntq += __shfl_xor(ntq, o);
+  const int items = p.num_kv_heads * __builtin_amdgcn_readfirstlane(ntq);
+  const int cap = min(p.split_slots, max(0, p.split_cus + p.split_cus / kSplitSpareDiv - items)) / p.num_kv_heads;
+  if (cap == 0) {
+    const int gx = p.num_seqs * p.num_kv_heads;
+    if (c >= gx * p.num_q_tiles) return ci;
+    const int x = c % gx;
+    ci.s = x / p.num_kv_heads;
+    ci.kvh = x - ci.s * p.num_kv_heads;
+    ci.t = p.num_q_tiles - 1 - c / gx;
+    return ci;  // may be a tile past the sequence's end: item_desc marks it invalid
+  }
+  ci.kvh = c % p.num_kv_heads;
+  const int k = c / p.num_kv_heads;
+  for (int t = p.num_q_tiles - 1; t >= 0; --t) {
+    for (int c0 = 0; c0 < p.num_seqs; c0 += 64) {
+      const int sq = c0 + lane;
+      bool alive = false, cand = false;
+      if (sq < p.num_seqs) {
+        const int Lq = c0 == 0 ? lq0 : p.cu_q[sq + 1] - p.cu_q[sq];
+        const int Lk = c0 == 0 ? lk0 : p.cu_k[sq + 1] - p.cu_k[sq];
+        alive = t * BP < Lq;
+        cand = alive && min(Lk, min((t + 1) * BP, Lq) + Lk - Lq) > thr;
+      }
+      const uint64_t am = __builtin_amdgcn_ballot_w64(alive);
+      const uint64_t cm = __builtin_amdgcn_ballot_w64(cand);
+      const int rank = cands + lanes_below(cm);
+      const bool sp = cand && rank < cap;
+      const uint64_t sm = __builtin_amdgcn_ballot_w64(sp);
+      const int n = __builtin_popcountll(am) + __builtin_popcountll(sm);
+      if (k < pos + n) {
+        const int first = pos + lanes_below(am) + lanes_below(sm);  // this lane's first position
+        const uint64_t hm = __builtin_amdgcn_ballot_w64(alive && k >= first && k < first + (sp ? 2 : 1));
+        if (hm == 0) return ci;  // cannot happen: the level's positions are the lanes' runs
+        const int L = static_cast<int>(__builtin_ctzll(hm));
+        ci.s = c0 + L;
+        ci.t = t;
+        ci.half = __builtin_amdgcn_readlane(k - first, L);
+        ci.pair = __builtin_amdgcn_readlane(sp ? rank : -1, L);
+        return ci;
+      }
+      pos += n;
+      cands += __builtin_popcountll(cm);
+    }
+  }
+  return ci;
+}
+
+// Restrict item d to key half `half` of its tiles: half 0 takes tiles
+// [0, mid), half 1 [mid, ntiles).  The item's keys are re-based at the half's
+// first key (k_start and Lk move together, so the causal offset Lk - Lq
+// follows), and kmax stops at the half's end.
+__device__ __forceinline__ void key_half(ItemDesc& d, int half, int slot) {
+  const int mid = (d.ntiles + 1) / 2;
+  const int t_lo = half ? mid : 0;
+  const int t_hi = half ? d.ntiles : mid;
+  const int k0 = t_lo * kBK;
+  d.kmax = min(d.kmax, t_hi * kBK) - k0;
+  d.ntiles = t_hi - t_lo;
+  d.k_start += k0;
+  d.Lk -= k0;
+  d.split_slot = slot;
+}
+
+// Bound on the merging workgroup's wait for the other half's partial.  That
+// half has already counted itself finished, so only its stores remain and the
+// wait ends within microseconds; the bound only keeps a wave from spinning
+// for ever should that ever fail.
+constexpr int kSplitSpinMax = 1 << 20;
+
+// End of one key half of a split item, after the loop: the workgroup that
+// finishes first writes its unnormalised O, row maxima and row sums to the
+// item's slot and returns false; the second waits for them, folds them into
+// its own acc and l (both rescaled to the larger maximum) and returns true.
+// It also zeroes the slot's control words for the next call.
+template <int D>
+__device__ __forceinline__ bool merge_key_halves(const PrefillParams& p, char* smem_all, int slot,
+                                                 f32x16 (&acc)[D / 32], float m_run, float& l) {
+  constexpr int NJD = D / 32;
+  constexpr int kThreads = 64 * kWaves;
+  uint32_t* ctl = p.split_ctl + 2 * slot;
+  float* part = p.split_part + static_cast<int64_t>(slot) * kPrefillSplitPartFloats;
+  float4* pacc = reinterpret_cast<float4*>(part);
+  float* pm = part + kRows * 128;
+  const int tid = threadIdx.x;
+  int* s_role = reinterpret_cast<int*>(smem_all);
+  barrier_lds();  // every wave is done with the ring
+  if (tid == 0) *s_role = static_cast<int>(atomicAdd(ctl, 1u));
+  barrier_lds();
+  const int role = __builtin_amdgcn_readfirstlane(*s_role);
+  if (role == 0) {
+#pragma unroll
+    for (int jd = 0; jd < NJD; ++jd)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        pacc[(4 * jd + b) * kThreads + tid] =
+            float4{acc[jd][4 * b], acc[jd][4 * b + 1], acc[jd][4 * b + 2], acc[jd][4 * b + 3]};
+    pm[tid] = m_run;
+    pm[kThreads + tid] = l;
+    // Every wave waits for its stores to reach L2, then one release at device
+    // scope publishes them all: an agent-scope fence writes back the whole L2
+    // of this XCD, so one per workgroup rather than one per wave.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    barrier_lds();
+    if (tid == 0) __hip_atomic_store(ctl + 1, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    return false;
+  }
+  if (tid == 0) {
+    // Poll with relaxed loads (an acquire per poll would invalidate this XCD's
+    // L2 each time, under every other workgroup on it), then acquire once.
+    for (int k = 0; k < kSplitSpinMax &&
+                    __hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u; ++k)
+      __builtin_amdgcn_s_sleep(2);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    __hip_atomic_store(ctl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ctl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  barrier_lds();
+  // the other waves' loads of the partial come after thread 0's acquire (the
+  // barrier orders them); a workgroup-scope acquire keeps them after it
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  // a half whose rows saw no key (sum 0) has no maximum: weight 0
+  const float la = pm[kThreads + tid];
+  const float ma = la > 0.f ? pm[tid] : kNegInf;
+  const float mb = l > 0.f ? m_run : kNegInf;
+  const float mm = fmaxf(ma, mb);
+  const float wa = ma == kNegInf ? 0.f : fast_exp2(ma - mm);
+  const float wb = mb == kNegInf ? 0.f : fast_exp2(mb - mm);
+  l = wa * la + wb * l;
+#pragma unroll
+  for (int jd = 0; jd < NJD; ++jd)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const float4 a = pacc[(4 * jd + b) * kThreads + tid];
+      acc[jd][4 * b] = wa * a.x + wb * acc[jd][4 * b];
+      acc[jd][4 * b + 1] = wa * a.y + wb * acc[jd][4 * b + 1];
+      acc[jd][4 * b + 2] = wa * a.z + wb * acc[jd][4 * b + 2];
+      acc[jd][4 * b + 3] = wa * a.w + wb * acc[jd][4 * b + 3];
+    }
+  return true;
 }
 
 // The thread index passes through an empty asm so that everything derived
@@ -572,7 +771,8 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
   // The next item's Q operands first: the last QK has been issued, so qop is
   // free, and the loads have the epilogue to land.
   if (next.valid) item_fetch_q<D>(p, next, qop);
-  const float l = sum_across_halves(l_run[0] + l_run[1]);
+  float l = sum_across_halves(l_run[0] + l_run[1]);
+  if (item.split_slot >= 0 && !merge_key_halves<D>(p, smem_all, item.split_slot, acc, m_run, l)) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   barrier_lds();  // every wave is done with the ring
   // stages 0 and 1 take the next item's first tiles
@@ -618,11 +818,26 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
 template <bool PAGED, int D>
 __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(1024))) char smem_all[kStages * Geom<D>::kStageBytes];
-  const int s = blockIdx.x / p.num_kv_heads;
-  const int kvh = blockIdx.x - s * p.num_kv_heads;
-  const int tile = p.num_q_tiles - 1 - static_cast<int>(blockIdx.y);
-  const ItemDesc it = item_desc(p, p.cu_q, p.cu_k, s, kvh, tile);
+  int s, kvh, tile, half = 0, pair = -1;
+  if (!PAGED && p.split_tiles > 0) {
+    // key halving: the compact grid (the real items first, heaviest first;
+    // one kv head's items on one XCD when num_kv_heads is a multiple of 8),
+    // or the plain one when nothing can split
+    const CellItem ci = compact_cell(p, static_cast<int>(blockIdx.x));
+    if (ci.s < 0) return;
+    s = ci.s;
+    kvh = ci.kvh;
+    tile = ci.t;
+    half = ci.half;
+    pair = ci.pair;
+  } else {
+    s = blockIdx.x / p.num_kv_heads;
+    kvh = blockIdx.x - s * p.num_kv_heads;
+    tile = p.num_q_tiles - 1 - static_cast<int>(blockIdx.y);
+  }
+  ItemDesc it = item_desc(p, p.cu_q, p.cu_k, s, kvh, tile);
   if (!it.valid) return;
+  if (pair >= 0) key_half(it, half, pair * p.num_kv_heads + kvh);
   bf16x8 qop[D / 16];
   item_fetch_q<D>(p, it, qop);
   item_fetch_tiles<PAGED, D>(p, smem_all, it);
@@ -823,7 +1038,16 @@ static int device_cu_count() {
   return counts[dev];
 }
 
-hipError_t launch_prefill(const PrefillParams& p0, int max_seqlen_q, hipStream_t stream) {
+// Key halving of the direct grid (packed k/v, with a workspace): with at most
+// two grid cells per CU, the longest items set the launch's length while CUs
+// sit idle.  Items of at least kSplitNum / kSplitDen of the longest key span
+// (and at least kSplitMin tiles) then run as two key halves, on the compact
+// grid (compact_cell).
+constexpr int kSplitNum = 3;
+constexpr int kSplitDen = 5;
+constexpr int kSplitMin = 8;
+
+hipError_t launch_prefill(const PrefillParams& p0, int max_seqlen_q, int max_seqlen_k, hipStream_t stream) {
   if (p0.num_seqs <= 0 || max_seqlen_q <= 0) return hipSuccess;
   PrefillParams p = p0;
   p.positions_per_tile = prefill_positions_per_tile(p.group);
@@ -856,7 +1080,21 @@ hipError_t launch_prefill(const PrefillParams& p0, int max_seqlen_q, hipStream_t
 #undef NVA_PERSIST
     return hipGetLastError();
   }
-  const dim3 grid(static_cast<unsigned>(p.num_seqs * p.num_kv_heads), static_cast<unsigned>(p.num_q_tiles));
+  // max_seqlen_k only sizes the cut: a wrong value changes which items are
+  // split, never the result beyond rounding
+  const int64_t kt_max = (std::max<int64_t>(max_seqlen_k, 0) + kBK - 1) / kBK;
+  p.split_tiles = 0;
+  p.split_slots = kPrefillSplitSlots;
+  p.split_cus = cus;
+  const int64_t pairs_split = kPrefillSplitSlots / p.num_kv_heads;  // at most this many pairs split
+  if (p.split_ctl != nullptr && p.split_part != nullptr && p.block_table == nullptr && max_items <= 2 * int64_t{cus} &&
+      kt_max >= kSplitMin && pairs_split > 0)
+    p.split_tiles = static_cast<int>(std::max<int64_t>(kSplitMin, (kSplitNum * kt_max + kSplitDen - 1) / kSplitDen));
+  // compact grid with key halving: every (sequence, tile) pair's position, one
+  // more for each pair that may split
+  const dim3 grid = p.split_tiles > 0
+                        ? dim3(static_cast<unsigned>(max_items + pairs_split * p.num_kv_heads))
+                        : dim3(static_cast<unsigned>(p.num_seqs * p.num_kv_heads), static_cast<unsigned>(p.num_q_tiles));
   if (p.head_dim == 64) {
     if (p.block_table)
       hipLaunchKernelGGL((varlen_prefill_kernel<true, 64>), grid, dim3(kThreads), 0, stream, p);

@@ -43,9 +43,10 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-# One prefill work-queue workspace per (device, stream): zeroed once, and every
-# completed nva_prefill call leaves it zero again.  Calls on one stream run one
-# after another, so they can share it; different streams get their own.
+# One prefill workspace per (device, stream) -- the work queue, and the
+# control words and partials of the key halves -- zeroed once: every completed
+# nva_prefill call leaves its control words zero again.  Calls on one stream
+# run one after another, so they can share it; different streams get their own.
 _PREFILL_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 
 

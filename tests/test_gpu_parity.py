@@ -748,14 +748,58 @@ def test_prefill_work_queue_matches_static_order(dev, monkeypatch):
         print(f"work queue vs static: {case.name if hasattr(case, 'name') else 'case'}", flush=True)
         queued = _run_prefill(case)
         ws = A._PREFILL_WORKSPACES[(dev.index or 0, torch.cuda.current_stream(dev).cuda_stream)]
-        assert int(ws.count_nonzero()) == 0, "the queue must be left zero"
+        assert int(ws[:_WS_CTL_BYTES].count_nonzero()) == 0, "the queue must be left zero"
         monkeypatch.setattr(A, "_prefill_workspace", lambda device, stream: None)
         static = _run_prefill(case, store=False)
         monkeypatch.setattr(A, "_prefill_workspace", orig)
         assert np.array_equal(queued, static)
         again = _run_prefill(case, store=False)
         assert np.array_equal(again, queued)
-        assert int(ws.count_nonzero()) == 0
+        assert int(ws[:_WS_CTL_BYTES].count_nonzero()) == 0
+
+
+# The prefill workspace's control words (the work queue, then the key-halving
+# slots' finish counts and ready flags) fill its first 1024 bytes; the rest holds
+# the key halves' partial results and is overwritten by every split call.
+_WS_CTL_BYTES = 1024
+
+
+@pytest.mark.parametrize("lens,nh,nkv,d", [
+    ([512, 540, 147, 296, 319, 300, 927, 255], 16, 8, 128),  # config 2's lengths
+    ([1000] * 8, 16, 8, 128),  # 512 items: no CU left free, so the compact grid runs every item whole
+    ([1000] * 6, 8, 1, 128),  # 84 pairs of >= 10 key tiles, 64 of them split (the workspace's slots)
+    ([900, 37, 0, 650], 14, 2, 64),  # GQA 7 (36 positions per tile), head_dim 64, an empty sequence
+    ([2048], 32, 8, 128),  # one fresh prompt (Qwen3-8B heads): 256 items, the 4 heaviest levels split
+])
+def test_prefill_key_halves(dev, monkeypatch, lens, nh, nkv, d):
+    """A direct-grid launch (at most two grid cells per CU) over packed k/v runs
+    on the compact grid, heaviest items first, and its items of many key tiles
+    as two workgroups, one per key half; the one that finishes second merges the
+    other's float32 partial (O, row maximum and sum) from the mirror's
+    workspace.  Without a workspace every item runs whole on the plain grid.
+    Both against the oracle on every row (the early rows of an item see no key of
+    its second half), the halves within the bf16 bar of the whole items, the
+    control words zero after each call, and a second call reusing the slots."""
+    from nanovllm_amd import workloads as W
+    from nanovllm_amd.layers import attention as A
+    pages = sum(-(-x // 256) for x in lens) + 4
+    case = W.make_prefill_case(lens, nh, nkv, pages, head_dim=d, seed=sum(lens) + d, bulk_device=dev)
+    assert case.block_tables is None
+    bp = 256 // (nh // nkv)
+    assert len(lens) * nkv * -(-max(lens) // bp) <= 2 * 256  # the direct grid serves this call
+    print(f"key halves lens={lens} nh={nh} nkv={nkv} d={d}", flush=True)
+    halved = _run_prefill(case)
+    ws = A._PREFILL_WORKSPACES[(dev.index or 0, torch.cuda.current_stream(dev).cuda_stream)]
+    assert int(ws[:_WS_CTL_BYTES].count_nonzero()) == 0, "the split slots must be left zero"
+    ref = prefill_reference(case)
+    assert_attn_close(halved, ref, what=f"key halves {lens}")
+    again = _run_prefill(case, store=False)
+    assert int(ws[:_WS_CTL_BYTES].count_nonzero()) == 0
+    assert_attn_close(again, ref, what=f"key halves, second call {lens}")
+    monkeypatch.setattr(A, "_prefill_workspace", lambda device, stream: None)
+    whole = _run_prefill(case, store=False)
+    assert_attn_close(whole, ref, what=f"whole items {lens}")
+    assert float(np.abs(halved - whole).max()) < 2e-2
 
 
 @pytest.mark.parametrize("prefix", [0, 256])
