@@ -92,7 +92,8 @@ int nva_store_kvcache(const void* key, int64_t key_row_stride,
  * workspace: NULL, or nva_prefill_workspace_bytes() bytes (about 8.7 MB), 256-byte aligned,
  *   holding zeros before its first use.  With it, a prefill over many work items hands
  *   them out dynamically (a work queue per XCD), and a prefill over few items (at most two
- *   per CU) of packed k/v runs its longest items as two halves of their key range, merged
+ *   per CU; paged caches with blocks of at most 512 keys) runs its longest items as two
+ *   halves of their key range (cut at a page boundary when paged), merged
  *   in the launch through float32 partials kept in the workspace.  Every completed call
  *   leaves the workspace's control words zero again, so it is allocated and cleared once
  *   and reused.  Calls that may run at the same time (different streams) need different

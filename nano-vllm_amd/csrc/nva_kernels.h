@@ -86,7 +86,7 @@ struct PrefillParams {
   int32_t head_dim;           // 64 or 128
   float scale_log2;
   uint32_t* queue;            // null: static item order; else kPrefillQueueWords zeroed words
-  // Key halving of the direct grid (packed k/v): items of at least split_tiles
+  // Key halving of the direct grid: items of at least split_tiles
   // key tiles (0: off) run as two workgroups over the two halves of their key
   // tiles, merged by the one that finishes second.  At most split_slots such
   // items; each has two zeroed control words in split_ctl and

@@ -122,12 +122,12 @@ __device__ __forceinline__ StageLane<Geom<D>::P> stage_lane(int w, int lane, int
 
 typedef const __attribute__((address_space(4))) int32_t const_i32;
 
-// Block id of the page holding key kb (-1 past the table's width).  The block
-// table is read through the constant address space: a scalar load, counted by
-// lgkmcnt, not vmcnt.
-__device__ __forceinline__ int page_of(const PrefillParams& p, const_i32* bt, int kb) {
+// Block id of the page holding key kb (-1 past the mb entries of the table row
+// at bt).  The block table is read through the constant address space: a
+// scalar load, counted by lgkmcnt, not vmcnt.
+__device__ __forceinline__ int page_of(const PrefillParams& p, const_i32* bt, int mb, int kb) {
   const int bi = kb / p.block_size;
-  return bi < p.max_blocks ? bt[bi] : -1;
+  return bi < mb ? bt[bi] : -1;
 }
 
 // Address of the first key of the 64-key tile at kb: packed K/V from
@@ -200,6 +200,7 @@ struct ItemDesc {
   int kmax;    // keys [0, kmax) are visible to some row of the tile
   int ntiles;  // 64-key tiles spanning [0, kmax)
   int split_slot;  // >= 0: one key half of a split item (workspace slot); -1: a whole item
+  int bt_off;      // paged: block-table entries before the item's first key (a second key half)
   bool valid;  // false: no item (s < 0) or a tile past the sequence's end
 };
 
@@ -211,6 +212,7 @@ __device__ __forceinline__ ItemDesc item_desc(const PrefillParams& p, const int*
   d.kvh = kvh;
   d.tile = tile;
   d.split_slot = -1;
+  d.bt_off = 0;
   d.valid = false;
   if (s < 0) return d;
   d.q_start = __builtin_amdgcn_readfirstlane(cu_q[s]);
@@ -234,10 +236,14 @@ __device__ __forceinline__ ItemDesc item_desc(const PrefillParams& p, const int*
 // split pair takes two consecutive positions, its key halves.  A pair splits
 // when its tile sees at least split_tiles key tiles (keys [0, min(Lk,
 // (t + 1) BP + Lk - Lq))) and fewer such pairs precede it in this order than
-// the cap: split_slots / num_kv_heads, and the CUs the real items leave free
-// (split_cus + split_cus / kSplitSpareDiv - items, over num_kv_heads): a half
-// beyond those waits for a CU, and an oversubscribed launch has no idle CU
-// for it to fill.  Its slots are rank * num_kv_heads + kv head.
+// the cap: split_slots / num_kv_heads, and the CUs the real items leave free,
+// over num_kv_heads: a half beyond those waits for a CU, and an oversubscribed
+// launch has no idle CU for it to fill.  When the lightest item sees at most
+// half the key tiles of the heaviest, split_cus / kSplitSpareDiv more may
+// split: the items that then wait for a CU are the lightest ones, which fit
+// beside the halves (with a long cached prefix every item is heavy, and a
+// waiting one would end after the halves).  Its slots are rank *
+// num_kv_heads + kv head.
 // Every workgroup derives it from cu_seqlens with ballots over 64 sequences at
 // a time, so the result is wave-uniform; s = -1 past the last pair.  (The
 // scan over the levels costs the lighter items time that an oversubscribed
@@ -272,17 +278,32 @@ __device__ __forceinline__ CellItem compact_cell(const PrefillParams& p, int c) 
     lq0 = p.cu_q[lane + 1] - p.cu_q[lane];
     lk0 = p.cu_k[lane + 1] - p.cu_k[lane];
   }
-  // real items: num_kv_heads * the sequences' query tiles
-  int ntq = lq0 > 0 ? (lq0 + BP - 1) / BP : 0;
+  // real items (num_kv_heads * the sequences' query tiles), and the keys the
+  // lightest (a sequence's first tile) and the heaviest (its last) item see
+  auto lens_stats = [&](int lq, int lk, int& ntq, int& kmin, int& kmax) {
+    if (lq > 0) {
+      ntq += (lq + BP - 1) / BP;
+      kmin = min(kmin, min(lk, min(BP, lq) + lk - lq));
+      kmax = max(kmax, lk);
+    }
+  };
+  int ntq = 0, kmin = 0x7fffffff, kmax = 0;
+  lens_stats(lq0, lk0, ntq, kmin, kmax);
   for (int c0 = 64; c0 < p.num_seqs; c0 += 64) {
     const int sq = c0 + lane;
-    const int lq = sq < p.num_seqs ? p.cu_q[sq + 1] - p.cu_q[sq] : 0;
-    ntq += lq > 0 ? (lq + BP - 1) / BP : 0;
+    if (sq < p.num_seqs) lens_stats(p.cu_q[sq + 1] - p.cu_q[sq], p.cu_k[sq + 1] - p.cu_k[sq], ntq, kmin, kmax);
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) ntq += __shfl_xor(ntq, o);
+  for (int o = 32; o > 0; o >>= 1) {
+    ntq += __shfl_xor(ntq, o);
+    kmin = min(kmin, __shfl_xor(kmin, o));
+    kmax = max(kmax, __shfl_xor(kmax, o));
+  }
   const int items = p.num_kv_heads * __builtin_amdgcn_readfirstlane(ntq);
-  const int cap = min(p.split_slots, max(0, p.split_cus + p.split_cus / kSplitSpareDiv - items)) / p.num_kv_heads;
+  const int kmin_u = __builtin_amdgcn_readfirstlane(min(kmin, 1 << 30));  // no sequence with queries: 2^30
+  const bool light_tail = 2 * ((kmin_u + kBK - 1) / kBK) <= (__builtin_amdgcn_readfirstlane(kmax) + kBK - 1) / kBK;
+  const int spare = p.split_cus + (light_tail ? p.split_cus / kSplitSpareDiv : 0) - items;
+  const int cap = min(p.split_slots, max(0, spare)) / p.num_kv_heads;
   if (cap == 0) {
     const int gx = p.num_seqs * p.num_kv_heads;
     if (c >= gx * p.num_q_tiles) return ci;
@@ -331,13 +352,23 @@ __device__ __forceinline__ CellItem compact_cell(const PrefillParams& p, int c) 
 // Restrict item d to key half `half` of its tiles: half 0 takes tiles
 // [0, mid), half 1 [mid, ntiles).  The item's keys are re-based at the half's
 // first key (k_start and Lk move together, so the causal offset Lk - Lq
-// follows), and kmax stops at the half's end.
-__device__ __forceinline__ void key_half(ItemDesc& d, int half, int slot) {
-  const int mid = (d.ntiles + 1) / 2;
+// follows), and kmax stops at the half's end.  Paged, mid is the page
+// boundary nearest the middle (tiles per page tpp; a tile never straddles
+// pages), and the second half starts mid / tpp entries into the block-table
+// row; mid may reach ntiles, leaving the second half no key (its partial then
+// weighs nothing in the merge).
+template <bool PAGED>
+__device__ __forceinline__ void key_half(const PrefillParams& p, ItemDesc& d, int half, int slot) {
+  int mid = (d.ntiles + 1) / 2;
+  if constexpr (PAGED) {
+    const int tpp = p.block_size / kBK;
+    mid = min(d.ntiles, max(tpp, (mid + tpp / 2) / tpp * tpp));
+    d.bt_off = half ? mid / tpp : 0;
+  }
   const int t_lo = half ? mid : 0;
   const int t_hi = half ? d.ntiles : mid;
   const int k0 = t_lo * kBK;
-  d.kmax = min(d.kmax, t_hi * kBK) - k0;
+  d.kmax = max(0, min(d.kmax, t_hi * kBK) - k0);
   d.ntiles = t_hi - t_lo;
   d.k_start += k0;
   d.Lk -= k0;
@@ -459,6 +490,7 @@ __device__ __forceinline__ void item_fetch_q(const PrefillParams& p, const ItemD
 template <bool PAGED, int D>
 struct ItemStaging {
   const_i32* bt;
+  int mb;  // entries of the block-table row from bt on
   const uint16_t* dbase;
   int64_t dstride;
   StageLane<Geom<D>::P> dl;
@@ -470,7 +502,8 @@ struct ItemStaging {
     const int tid = laundered_tid();
     w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: staging bases stay scalar
     const bool k_wave = w < 4;
-    bt = PAGED ? (const_i32*)(p.block_table + static_cast<int64_t>(it.s) * p.bt_row_stride) : nullptr;
+    bt = PAGED ? (const_i32*)(p.block_table + static_cast<int64_t>(it.s) * p.bt_row_stride + it.bt_off) : nullptr;
+    mb = p.max_blocks - it.bt_off;
     dbase = (k_wave ? p.k : p.v) + it.kvh * D;
     dstride = k_wave ? p.k_row_stride : p.v_row_stride;
     dl = stage_lane<D>(w, tid & 63, dstride);
@@ -496,7 +529,7 @@ __device__ __forceinline__ void item_fetch_tiles(const PrefillParams& p, char* s
   const ItemStaging<PAGED, D> st(p, it);
 #pragma unroll
   for (int t = 0; t < 2; ++t)
-    if (t < it.ntiles) st.copy(p, it, smem_all + t * Geom<D>::kTileBytes, PAGED ? page_of(p, st.bt, t * kBK) : 0, t);
+    if (t < it.ntiles) st.copy(p, it, smem_all + t * Geom<D>::kTileBytes, PAGED ? page_of(p, st.bt, st.mb, t * kBK) : 0, t);
 }
 
 // Run work item `it` on the whole workgroup.  Its Q operands (qop) and the
@@ -689,7 +722,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
   const int64_t tile_step = static_cast<int64_t>(kBK) * stg.dstride * 2;
   const int tpp = PAGED ? p.block_size / kBK : 1;  // tiles per page
   const uint32_t nb32 = p.num_blocks > 0x7fffffff ? 0x7fffffffu : static_cast<uint32_t>(p.num_blocks);
-  auto page_at = [&](int idx) { return idx < p.max_blocks ? stg.bt[idx] : -1; };
+  auto page_at = [&](int idx) { return idx < stg.mb ? stg.bt[idx] : -1; };
   auto page_base = [&](int page) {
     const int64_t slot = static_cast<uint32_t>(page) < nb32 ? static_cast<int64_t>(page) * p.block_size : 0;
     return reinterpret_cast<const char*>(stg.dbase + slot * stg.dstride);
@@ -819,7 +852,7 @@ template <bool PAGED, int D>
 __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(1024))) char smem_all[kStages * Geom<D>::kStageBytes];
   int s, kvh, tile, half = 0, pair = -1;
-  if (!PAGED && p.split_tiles > 0) {
+  if (p.split_tiles > 0) {
     // key halving: the compact grid (the real items first, heaviest first;
     // one kv head's items on one XCD when num_kv_heads is a multiple of 8),
     // or the plain one when nothing can split
@@ -837,7 +870,7 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   }
   ItemDesc it = item_desc(p, p.cu_q, p.cu_k, s, kvh, tile);
   if (!it.valid) return;
-  if (pair >= 0) key_half(it, half, pair * p.num_kv_heads + kvh);
+  if (pair >= 0) key_half<PAGED>(p, it, half, pair * p.num_kv_heads + kvh);
   bf16x8 qop[D / 16];
   item_fetch_q<D>(p, it, qop);
   item_fetch_tiles<PAGED, D>(p, smem_all, it);
@@ -1038,7 +1071,7 @@ static int device_cu_count() {
   return counts[dev];
 }
 
-// Key halving of the direct grid (packed k/v, with a workspace): with at most
+// Key halving of the direct grid (with a workspace): with at most
 // two grid cells per CU, the longest items set the launch's length while CUs
 // sit idle.  Items of at least kSplitNum / kSplitDen of the longest key span
 // (and at least kSplitMin tiles) then run as two key halves, on the compact
@@ -1046,6 +1079,7 @@ static int device_cu_count() {
 constexpr int kSplitNum = 3;
 constexpr int kSplitDen = 5;
 constexpr int kSplitMin = 8;
+constexpr int kSplitMaxPageTiles = 8;  // paged key halving for block sizes up to 512
 
 hipError_t launch_prefill(const PrefillParams& p0, int max_seqlen_q, int max_seqlen_k, hipStream_t stream) {
   if (p0.num_seqs <= 0 || max_seqlen_q <= 0) return hipSuccess;
@@ -1087,9 +1121,13 @@ hipError_t launch_prefill(const PrefillParams& p0, int max_seqlen_q, int max_seq
   p.split_slots = kPrefillSplitSlots;
   p.split_cus = cus;
   const int64_t pairs_split = kPrefillSplitSlots / p.num_kv_heads;  // at most this many pairs split
-  if (p.split_ctl != nullptr && p.split_part != nullptr && p.block_table == nullptr && max_items <= 2 * int64_t{cus} &&
-      kt_max >= kSplitMin && pairs_split > 0)
-    p.split_tiles = static_cast<int>(std::max<int64_t>(kSplitMin, (kSplitNum * kt_max + kSplitDen - 1) / kSplitDen));
+  // paged: the halves meet at a page boundary, so only items of at least two
+  // pages' tiles split (tpp tiles per page; pages of at most kSplitMaxPageTiles)
+  const int tpp = p.block_table ? p.block_size / kBK : 1;
+  if (p.split_ctl != nullptr && p.split_part != nullptr && max_items <= 2 * int64_t{cus} && kt_max >= kSplitMin &&
+      pairs_split > 0 && tpp <= kSplitMaxPageTiles)
+    p.split_tiles = static_cast<int>(
+        std::max<int64_t>(std::max(kSplitMin, 2 * tpp), (kSplitNum * kt_max + kSplitDen - 1) / kSplitDen));
   // compact grid with key halving: every (sequence, tile) pair's position, one
   // more for each pair that may split
   const dim3 grid = p.split_tiles > 0

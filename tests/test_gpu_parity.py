@@ -509,6 +509,42 @@ def test_prefill_group_16_prefix(dev, prefix):
     assert_attn_close(got, prefill_reference(case), what=f"group 16 prefix={prefix}")
 
 
+@pytest.mark.parametrize("lens,prefix,nh,nkv,d,bs", [
+    (None, 1024, 4, 1, 128, 256),  # config 4's lengths at heads 4/1 (one GPU's share at TP8)
+    ([700, 300, 1000], [512, 0, 256], 16, 8, 128, 64),  # one tile per page, mixed prefixes
+    ([900, 400], [1024, 512], 32, 8, 128, 512),  # eight tiles per page
+    ([1500, 600], [256, 0], 14, 2, 64, 128),  # GQA 7, head_dim 64
+])
+def test_prefill_key_halves_paged(dev, monkeypatch, lens, prefix, nh, nkv, d, bs):
+    """Prefix-cached (paged) direct-grid launches with key halving: a split
+    item's halves meet at the page boundary nearest its middle, and the second
+    half reads the block-table row from that page on.  Every row against the
+    oracle and against whole items (no workspace); the control words zero."""
+    from nanovllm_amd import workloads as W
+    from nanovllm_amd.layers import attention as A
+    gen = None
+    if lens is None:
+        gen = torch.Generator().manual_seed(W.SEEDS[4])
+        lens = torch.randint(256, 769, (16,), generator=gen).tolist()
+    pre = prefix if isinstance(prefix, list) else [prefix] * len(lens)
+    pages = sum(-(-(q + x) // bs) for q, x in zip(lens, pre)) + 4
+    case = W.make_prefill_case(lens, nh, nkv, pages, prefix_len=pre, block_size=bs, head_dim=d,
+                               seed=sum(lens) + bs, bulk_device=dev, shared_prefix=False, gen=gen)
+    assert case.block_tables is not None
+    bp = 256 // (nh // nkv)
+    assert len(lens) * nkv * -(-max(lens) // bp) <= 2 * 256  # the direct grid serves this call
+    print(f"paged key halves lens={lens} prefix={prefix} nh={nh} nkv={nkv} d={d} bs={bs}", flush=True)
+    halved = _run_prefill(case)
+    ws = A._PREFILL_WORKSPACES[(dev.index or 0, torch.cuda.current_stream(dev).cuda_stream)]
+    assert int(ws[:_WS_CTL_BYTES].count_nonzero()) == 0, "the split slots must be left zero"
+    ref = prefill_reference(case)
+    assert_attn_close(halved, ref, what=f"paged key halves bs={bs}")
+    monkeypatch.setattr(A, "_prefill_workspace", lambda device, stream: None)
+    whole = _run_prefill(case, store=False)
+    assert_attn_close(whole, ref, what=f"paged whole items bs={bs}")
+    assert float(np.abs(halved - whole).max()) < 2e-2
+
+
 SPIKE_POSITIONS = (5, 37, 70, 100, 131, 250)  # spread over both lane halves and several steps
 
 
