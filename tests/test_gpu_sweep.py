@@ -7,6 +7,9 @@ through store_and_decode.  Prefill: the direct and the persistent grid, packed
 and paged (mixed cached prefixes, block sizes 64-512), GQA groups 1-7, head_dim 64
 and 128, ragged lengths including empty query segments.
 
+Key halving: 24 launches of a few long sequences (the direct grid, whose longest
+items then run as two key halves), packed and paged.
+
 The shapes are drawn once from fixed seeds, so every run checks the same cases;
 each is sized so the CPU oracle takes at most a few seconds.  Bars: bf16 within
 2e-2 max-abs / 2e-3 mean-abs, fp8 within 5e-2 of the oracle on the dequantised
@@ -71,6 +74,32 @@ def _prefill_shapes(n=30, seed=4048):
     return out
 
 
+def _split_shapes(n=24, seed=6060):
+    """Few long sequences (direct grid, at most two items per CU), so that the
+    longest items run as key halves: packed or paged at block sizes 64-512 with
+    mixed cached prefixes, GQA groups 1-16 over 1-8 kv heads."""
+    r = random.Random(seed)
+    out = []
+    while len(out) < n:
+        nkv = r.choice([1, 2, 4, 8])
+        group = r.choice([1, 2, 4, 7, 8, 16])
+        bp = 256 // group
+        S = r.randint(1, 6)
+        lens = [r.randint(1, 2000) for _ in range(S)]
+        lens[r.randrange(S)] = r.randint(600, 2000)
+        paged = r.random() < 0.5
+        bs = r.choice([64, 128, 256, 512]) if paged else 256
+        pre = [r.choice([0, bs, 2 * bs, 4 * bs]) for _ in range(S)] if paged else [0] * S
+        if S * nkv * -(-max(lens) // bp) > 512:  # the persistent grid would serve it
+            continue
+        work = sum(q * (q + x) for q, x in zip(lens, pre)) * group * nkv
+        if work > 1.5e8:  # keep the CPU oracle within seconds
+            continue
+        out.append(dict(i=len(out), nkv=nkv, nh=group * nkv, d=r.choice([64, 128]), lens=lens, pre=pre,
+                        paged=paged, bs=bs))
+    return out
+
+
 @pytest.mark.parametrize("shape", _decode_shapes(), ids=lambda s: f"d{s['i']}")
 def test_decode_sweep(dev, shape):
     import nanovllm_amd as nva
@@ -115,3 +144,20 @@ def test_prefill_sweep(dev, shape):
                                    case.cu_seqlens_k, case.scale, True, case.block_tables)
     torch.cuda.synchronize()
     assert_attn_close(f32(o), prefill_reference(case), what=f"prefill sweep {s}")
+
+
+@pytest.mark.parametrize("shape", _split_shapes(), ids=lambda s: f"k{s['i']}")
+def test_prefill_key_halves_sweep(dev, shape):
+    import nanovllm_amd as nva
+    from nanovllm_amd import workloads as W
+    s = shape
+    print(f"key halves sweep {s}", flush=True)
+    pages = sum(-(-(q + p) // s["bs"]) for q, p in zip(s["lens"], s["pre"])) + 4
+    case = W.make_prefill_case(s["lens"], s["nh"], s["nkv"], pages, prefix_len=s["pre"], block_size=s["bs"],
+                               head_dim=s["d"], seed=300 + s["i"], bulk_device=dev, shared_prefix=False)
+    nva.store_kvcache(case.k, case.v, case.k_cache, case.v_cache, case.slot_mapping)
+    k, v = (case.k, case.v) if case.block_tables is None else (case.k_cache, case.v_cache)
+    o = nva.flash_attn_varlen_func(case.q, k, v, case.max_seqlen_q, case.cu_seqlens_q, case.max_seqlen_k,
+                                   case.cu_seqlens_k, case.scale, True, case.block_tables)
+    torch.cuda.synchronize()
+    assert_attn_close(f32(o), prefill_reference(case), what=f"key halves sweep {s}")
