@@ -457,6 +457,13 @@ def main(argv=None):
         if not args.no_cpu:
             host["cfg2"] = W.config2("cpu")
         del c2
+        # one fresh 2048-token prompt at Qwen3-8B heads (packed, direct grid): the
+        # time-to-first-token case of a single request, no roofline claim
+        c1p = W.make_prefill_case([2048], 32, 8, 12, seed=2048, bulk_device=dev, name="single_prompt")
+        out["single_prompt"] = bench_prefill(c1p, max(10, steps // 2), warmup, args.warm_seconds)
+        log(f"[bench] one 2048-token prompt (heads 32/8): {out['single_prompt']['ms']*1e3:.1f} us "
+            f"= {out['single_prompt']['tflops']:.0f} TFLOP/s")
+        del c1p
         torch.cuda.empty_cache()
     if args.only in (None, "producer"):
         log("[bench] producer: fused qk-RMSNorm + rotary over config 4's 8813 tokens (heads 32/8)")
@@ -535,6 +542,12 @@ def main(argv=None):
                                "gflop": round(out[k]["flops"] / 1e9, 2),
                                "frac_bf16_peak": round(out[k]["tflops"] / BF16_PEAK_TFLOPS, 4)}
                            for k in ("cfg4", "cfg2") if k in out}
+    if "single_prompt" in out:
+        sp = out["single_prompt"]
+        line["prefill_single_prompt"] = {"note": "one fresh 2048-token prompt, heads 32/8, head_dim 128 (packed): "
+                                                 "time to first token of one request; no roofline claim",
+                                         "us": round(sp["ms"] * 1e3, 2), "tflops": round(sp["tflops"], 1),
+                                         "gflop": round(sp["flops"] / 1e9, 2)}
     if "store4" in out or "store2" in out:
         line["store_kvcache_prefill"] = {
             k: {"tokens": out[s]["tokens"], "us": round(out[s]["ms"] * 1e3, 2), "bytes": out[s]["bytes"],
