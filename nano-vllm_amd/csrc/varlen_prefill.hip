@@ -537,8 +537,10 @@ __device__ __forceinline__ void item_fetch_tiles(const PrefillParams& p, char* s
 // item_fetch_tiles).  When `next` is valid, this issues next's Q loads into
 // qop once the last QK has been issued and next's first two tile copies right
 // after the epilogue's barrier, so their latency overlaps the epilogue; the
-// epilogue's transpose therefore uses ring stages 2 and 3 only.
-template <bool PAGED, int D>
+// epilogue's transpose therefore uses ring stages 2 and 3 only.  SPLIT: the
+// item may be one key half, merged at the end (merge_key_halves); only the
+// direct grid splits, so the persistent grid's code carries no merge.
+template <bool PAGED, int D, bool SPLIT>
 __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_all, const ItemDesc& item,
                                             bf16x8 (&qop)[D / 16], const ItemDesc& next, uint32_t* claim_ctr,
                                             uint32_t& claim) {
@@ -805,7 +807,9 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, char* smem_a
   // free, and the loads have the epilogue to land.
   if (next.valid) item_fetch_q<D>(p, next, qop);
   float l = sum_across_halves(l_run[0] + l_run[1]);
-  if (item.split_slot >= 0 && !merge_key_halves<D>(p, smem_all, item.split_slot, acc, m_run, l)) return;
+  if constexpr (SPLIT) {
+    if (item.split_slot >= 0 && !merge_key_halves<D>(p, smem_all, item.split_slot, acc, m_run, l)) return;
+  }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   barrier_lds();  // every wave is done with the ring
   // stages 0 and 1 take the next item's first tiles
@@ -877,7 +881,7 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_kernel(PrefillPara
   ItemDesc none{};
   none.valid = false;
   uint32_t unused = 0;
-  prefill_run<PAGED, D>(p, smem_all, it, qop, none, nullptr, unused);
+  prefill_run<PAGED, D, true>(p, smem_all, it, qop, none, nullptr, unused);
 }
 
 // Persistent grid: one workgroup per CU walks the real work items.
@@ -1048,7 +1052,7 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(
       const int64_t item64 = static_cast<int64_t>(round) * NW + q;
       nxt = desc_of(item64 < total ? static_cast<int>(item64) : total);
     }
-    prefill_run<PAGED, D>(p, smem_all, cur, qop, nxt, claim_ctr, claim);
+    prefill_run<PAGED, D, false>(p, smem_all, cur, qop, nxt, claim_ctr, claim);
     if (!nxt.valid) break;
     cur = nxt;
   }
