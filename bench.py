@@ -15,7 +15,7 @@ path (store + gather + SDPA) timed on the host cores on a bounded sample of
 every configuration (`cpu_baseline` is config 3's, `cpu_baselines` all five).
 
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--warm-seconds 1] [--no-cpu]
-                       [--only decode|prefill|fp8|producer|graphs]
+                       [--only decode|prefill|fp8|producer|graphs|tp8]
 """
 from __future__ import annotations
 
@@ -227,6 +227,81 @@ def bench_store(case, steps, warmup, warm_s=1.0, n_pools=8):
                 frac=nbytes / (ms * 1e-3) / 8.0e12)
 
 
+def bench_copy(dev, steps, warm_s=0.25, nbytes=1 << 30):
+    """A plain device-to-device copy of 1 GiB (torch's copy kernel): the practical
+    read + write ceiling the store's scatter is compared with.  The 2 GiB footprint
+    exceeds the 256 MB Infinity Cache."""
+    import torch
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    _warm(lambda i: dst.copy_(src), 3, warm_s)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    del src, dst
+    return dict(ms=ms, bytes=2 * nbytes, gbs=2 * nbytes / (ms * 1e-3) / 1e9)
+
+
+def bench_prefill_fp8(case, steps, warmup, warm_s=1.0):
+    """A prefix-cached prefill over an fp8 e4m3fn cache (scales amax / 448 per kv head,
+    the cached prefix and the suffix quantised by store_kvcache): one
+    flash_attn_varlen_func call = nva_gather_kv of every sequence's pages into packed
+    dequantised bf16 rows + the packed prefill over them.  The gather is also timed
+    alone, on the same rows."""
+    import torch
+    import nanovllm_amd as nva
+    from nanovllm_amd import _capi, workloads as W
+    kc8, ks = W.quantize_cache_fp8(case.k_cache, extra=case.k)
+    vc8, vs = W.quantize_cache_fp8(case.v_cache, extra=case.v)
+    nva.store_kvcache(case.k, case.v, kc8, vc8, case.slot_mapping, ks, vs)
+    bt = case.block_tables
+
+    def run(i=0):
+        return nva.flash_attn_varlen_func(case.q, kc8, vc8, case.max_seqlen_q, case.cu_seqlens_q, case.max_seqlen_k,
+                                          case.cu_seqlens_k, case.scale, True, bt, k_scale=ks, v_scale=vs)
+
+    _warm(run, warmup, warm_s)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record()
+        run()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    S = len(case.lens_q)
+    nkv, d = case.num_kv_heads, case.head_dim
+    rows = S * case.max_seqlen_k
+    kp = torch.empty(rows, nkv, d, dtype=torch.bfloat16, device=case.q.device)
+    vp = torch.empty_like(kp)
+    lib = _capi.load()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def gather(i=0):
+        _capi.check(lib.nva_gather_kv(kc8.data_ptr(), vc8.data_ptr(), _capi.NVA_DTYPE_FP8_E4M3, ks.data_ptr(),
+                                      vs.data_ptr(), kc8.shape[0], bt.data_ptr(), bt.stride(0), bt.shape[1],
+                                      case.block_size, case.cu_seqlens_k.data_ptr(), S, case.max_seqlen_k, nkv, d,
+                                      kp.data_ptr(), vp.data_ptr(), rows, nkv * d, stream))
+
+    _warm(gather, warmup, warm_s / 4)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        gather()
+    e1.record()
+    torch.cuda.synchronize()
+    g_ms = e0.elapsed_time(e1) / steps
+    keys = sum(case.lens_k)
+    g_bytes = 2 * keys * nkv * d * (1 + 2) + 4 * sum(math.ceil(x / case.block_size) for x in case.lens_k)
+    flops = case.flops()
+    del kc8, vc8, kp, vp
+    return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12, gather_ms=g_ms, gather_bytes=g_bytes,
+                gather_gbs=g_bytes / (g_ms * 1e-3) / 1e9)
+
+
 def bench_producer(case, steps, warmup, warm_s=1.0):
     """The fused qk-RMSNorm + rotary step (nva_qk_norm_rope) over config 4's tokens."""
     import torch
@@ -322,9 +397,6 @@ def cpu_baseline_decode(case, name, budget_s):
     B = case.batch
     kw = dict(k_scale=case.k_scale, v_scale=case.v_scale)
     fp8 = case.k_scale is not None
-    kc, vc = case.k_cache, case.v_cache
-    if fp8:  # the byte copies of the store go through uint8 views of the same memory
-        kc, vc = kc.view(torch.uint8), vc.view(torch.uint8)
     probe = min(B, 2 if fp8 else 8)
     t0 = time.perf_counter()
     CB.decode(case.q[:probe], case.k_cache, case.v_cache, case.context_lens[:probe], case.block_tables[:probe],
@@ -334,10 +406,11 @@ def cpu_baseline_decode(case, name, budget_s):
 
     def step():
         k_new, v_new = case.k_new[:n], case.v_new[:n]
-        if fp8:  # the fp8 store: e4m3fn(x / scale), torch's cast (bit-identical to the kernel's)
-            k_new = (k_new.float() / case.k_scale.view(1, -1, 1)).to(torch.float8_e4m3fn).view(torch.uint8)
-            v_new = (v_new.float() / case.v_scale.view(1, -1, 1)).to(torch.float8_e4m3fn).view(torch.uint8)
-        CB.store_kvcache(k_new, v_new, kc, vc, case.slot_mapping[:n])
+        if fp8:  # e4m3fn(x / scale), torch's cast (bit-identical to the kernel's)
+            CB.store_kvcache_fp8(k_new, v_new, case.k_cache, case.v_cache, case.slot_mapping[:n],
+                                 case.k_scale, case.v_scale)
+        else:
+            CB.store_kvcache(k_new, v_new, case.k_cache, case.v_cache, case.slot_mapping[:n])
         CB.decode(case.q[:n], case.k_cache, case.v_cache, case.context_lens[:n], case.block_tables[:n],
                   case.scale, **kw)
 
@@ -387,7 +460,7 @@ def main(argv=None):
     ap.add_argument("--warm-seconds", type=float, default=1.0,
                     help="after the warmup steps, keep running each workload untimed for this long")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["decode", "prefill", "fp8", "producer", "graphs"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "fp8", "producer", "graphs", "tp8"], default=None)
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args(argv)
@@ -447,6 +520,16 @@ def main(argv=None):
         if not args.no_cpu:
             host["cfg4"] = W.config4("cpu")
         del c4
+        log("[bench] config 4 over an fp8 cache: gather + packed prefill")
+        c4 = W.config4(dev)
+        out["cfg4_fp8"] = bench_prefill_fp8(c4, max(10, steps // 2), warmup, args.warm_seconds)
+        log(f"[bench] cfg4 fp8 cache {out['cfg4_fp8']['ms']*1e3:.1f} us = {out['cfg4_fp8']['tflops']:.0f} TFLOP/s "
+            f"(gather alone {out['cfg4_fp8']['gather_ms']*1e3:.1f} us = {out['cfg4_fp8']['gather_gbs']:.0f} GB/s)")
+        del c4
+        torch.cuda.empty_cache()
+        out["copy"] = bench_copy(dev, 20, args.warm_seconds / 4)
+        log(f"[bench] plain 1 GiB device copy {out['copy']['ms']*1e3:.1f} us = {out['copy']['gbs']:.0f} GB/s "
+            f"(read + write)")
         log("[bench] config 2: varlen prefill")
         c2 = W.config2(dev)
         out["cfg2"] = bench_prefill(c2, max(10, steps // 2), warmup, args.warm_seconds)
@@ -478,6 +561,19 @@ def main(argv=None):
         for bs, r in out["graphs"].items():
             log(f"[bench] graph decode bs={bs}: {r['step_us']} us/step ({r['layer_us']} us/layer, "
                 f"{r['kv_gbs']} GB/s of KV)")
+        torch.cuda.empty_cache()
+    if args.only in (None, "tp8"):
+        log("[bench] TP8 shares: config 5 at heads 8/1 (fp8 decode), config 4 at heads 4/1 (prefix prefill)")
+        c5s = W.config5_tp8(dev)
+        out["cfg5_tp8"] = bench_decode(c5s, max(10, steps // 2), warmup, warm_s=args.warm_seconds)
+        log(f"[bench] cfg5 TP8 share attention {out['cfg5_tp8']['attn_ms']*1e3:.1f} us "
+            f"= {out['cfg5_tp8']['attn_gbs']:.0f} GB/s")
+        del c5s
+        torch.cuda.empty_cache()
+        c4s = W.config4_tp8(dev)
+        out["cfg4_tp8"] = bench_prefill(c4s, max(10, steps // 2), warmup, args.warm_seconds)
+        log(f"[bench] cfg4 TP8 share {out['cfg4_tp8']['ms']*1e3:.1f} us = {out['cfg4_tp8']['tflops']:.0f} TFLOP/s")
+        del c4s
         torch.cuda.empty_cache()
     if args.only in (None, "fp8"):
         log("[bench] config 5: fp8 KV decode, B=64, ctx U[16k,32k]")
@@ -537,11 +633,42 @@ def main(argv=None):
                                        "call per step",
                                "step_us": round(d1["step_ms"] * 1e3, 2), "call_us": round(d1["call_ms"] * 1e3, 2),
                                "gbs": round(d1["call_gbs"], 1), "bytes": d1["attn_bytes"] + d1["store_bytes"]}
+    if "cfg4" in out:
+        p4 = out["cfg4"]
+        line["prefill"] = {"config": "config 4: prefix-cached prefill, 16 sequences, 1024 cached + U[256,768] new "
+                                     "tokens, heads 32/8, head_dim 128, block_size 256",
+                           "tflops": round(p4["tflops"], 1), "ms": round(p4["ms"], 5),
+                           "frac": round(p4["tflops"] / BF16_PEAK_TFLOPS, 4), "gflop": round(p4["flops"] / 1e9, 2),
+                           "bound": "mfma", "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s"}
     if "cfg4" in out or "cfg2" in out:
-        line["prefill"] = {k: {"tflops": round(out[k]["tflops"], 1), "ms": round(out[k]["ms"], 4),
-                               "gflop": round(out[k]["flops"] / 1e9, 2),
-                               "frac_bf16_peak": round(out[k]["tflops"] / BF16_PEAK_TFLOPS, 4)}
-                           for k in ("cfg4", "cfg2") if k in out}
+        line["prefill_configs"] = {k: {"tflops": round(out[k]["tflops"], 1), "ms": round(out[k]["ms"], 5),
+                                       "gflop": round(out[k]["flops"] / 1e9, 2),
+                                       "frac_bf16_peak": round(out[k]["tflops"] / BF16_PEAK_TFLOPS, 4)}
+                                   for k in ("cfg4", "cfg2") if k in out}
+    if "cfg4_fp8" in out:
+        f = out["cfg4_fp8"]
+        line["prefill_fp8_cache"] = {"workload": "config 4 over an fp8 e4m3fn cache (per-kv-head scales): "
+                                                 "nva_gather_kv into packed bf16 rows + packed prefill, one call",
+                                     "us": round(f["ms"] * 1e3, 2), "tflops": round(f["tflops"], 1),
+                                     "frac_bf16_peak": round(f["tflops"] / BF16_PEAK_TFLOPS, 4),
+                                     "gather_us": round(f["gather_ms"] * 1e3, 2), "gather_bytes": f["gather_bytes"],
+                                     "gather_gbs": round(f["gather_gbs"], 1),
+                                     "gather_frac": round(f["gather_gbs"] / HBM_PEAK_GBS, 4)}
+    if "cfg5_tp8" in out or "cfg4_tp8" in out:
+        tp = {}
+        if "cfg5_tp8" in out:
+            r = out["cfg5_tp8"]
+            tp["cfg5"] = {"workload": "config 5 at heads 8/1 (one kv head), fp8 cache, B=64, ctx U[16k,32k]",
+                          "roofline": {"bound": "hbm", "achieved": round(r["attn_gbs"], 1), "peak": HBM_PEAK_GBS,
+                                       "unit": "GB/s", "frac": round(r["attn_gbs"] / HBM_PEAK_GBS, 4)},
+                          "attn_us": round(r["attn_ms"] * 1e3, 2), "bytes": r["attn_bytes"]}
+        if "cfg4_tp8" in out:
+            r = out["cfg4_tp8"]
+            tp["cfg4"] = {"workload": "config 4 at heads 4/1 (one kv head), prefix 1024 + U[256,768]",
+                          "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
+                                       "unit": "TFLOP/s", "frac": round(r["tflops"] / BF16_PEAK_TFLOPS, 4)},
+                          "us": round(r["ms"] * 1e3, 2), "gflop": round(r["flops"] / 1e9, 2)}
+        line["tp8_shares"] = tp
     if "single_prompt" in out:
         sp = out["single_prompt"]
         line["prefill_single_prompt"] = {"note": "one fresh 2048-token prompt, heads 32/8, head_dim 128 (packed): "
@@ -555,6 +682,10 @@ def main(argv=None):
                 "traffic": profiled_traffic(f"store_{k}", "store_hbm_traffic.md"),
                 "traffic_source": "profiles/store_hbm_traffic.md"}
             for k, s in (("cfg4", "store4"), ("cfg2", "store2")) if s in out}
+        if "copy" in out:
+            line["store_kvcache_prefill"]["copy_gbs"] = round(out["copy"]["gbs"], 1)
+            line["store_kvcache_prefill"]["copy_note"] = ("plain 1 GiB device-to-device copy (read + write bytes): "
+                                                          "the practical ceiling of a scatter")
     if "cfg5" in out:
         d5 = out["cfg5"]
         line["fp8_decode"] = {"cfg5": {"gbs": round(d5["attn_gbs"], 1), "frac": round(d5["attn_gbs"] / HBM_PEAK_GBS, 4),

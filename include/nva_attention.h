@@ -95,10 +95,16 @@ int nva_store_kvcache(const void* key, int64_t key_row_stride,
  *   per CU; paged caches with blocks of at most 512 keys) runs its longest items as two
  *   halves of their key range (cut at a page boundary when paged), merged
  *   in the launch through float32 partials kept in the workspace.  Every completed call
- *   leaves the workspace's control words zero again, so it is allocated and cleared once
- *   and reused.  Calls that may run at the same time (different streams) need different
- *   workspaces.  NULL selects a static item order and whole items: bit-identical to the
- *   work queue, and within float32 rounding of the halves (the merge reassociates sums).
+ *   leaves the workspace's control words consistent (queue counters zero; each half slot's
+ *   arrival count, ready word and epoch advanced together), so it is allocated and cleared
+ *   once and reused.  Calls that may run at the same time (different streams) need
+ *   different workspaces.  NULL selects a static item order and whole items: bit-identical
+ *   to the work queue, and within float32 rounding of the halves (the merge reassociates
+ *   sums).  Should a half's wait for the other half's partial ever give up (a bounded wait
+ *   of about 30 ms; words out of step), that item's rows are written as NaN and bit
+ *   NVA_PREFILL_ERR_SPLIT_WAIT is set in the workspace's error word (read and cleared by
+ *   nva_prefill_workspace_errors).  The 32-bit word at byte 132 of the workspace bounds
+ *   that wait: 0 (as zeroed) is the default bound, n > 0 allows n - 1 polls (a test hook).
  */
 int nva_prefill(const void* q, int64_t q_row_stride,
                 const void* k, int64_t k_row_stride,
@@ -114,6 +120,16 @@ int nva_prefill(const void* q, int64_t q_row_stride,
 
 /* Bytes of the optional nva_prefill workspace (a constant of the library). */
 int64_t nva_prefill_workspace_bytes(void);
+
+/*
+ * Error bits a prefill workspace has collected, copied to *errors and cleared (no
+ * counterpart in the reference, where flash-attn keeps no state between calls).
+ * NVA_PREFILL_ERR_SPLIT_WAIT: a key-half merge gave up waiting; that item's output rows
+ * were written as NaN.  Ordered on `stream` after the calls before it, and the one entry
+ * point that waits for the stream: for diagnostics and tests, not for captured graphs.
+ */
+#define NVA_PREFILL_ERR_SPLIT_WAIT 1u
+int nva_prefill_workspace_errors(void* workspace, int64_t workspace_bytes, uint32_t* errors, void* stream);
 
 /*
  * Workspace bytes nva_decode needs for these launch parameters (0 if it needs none).
@@ -154,15 +170,23 @@ int nva_decode(const void* q, int64_t q_row_stride,
  * head_dim) bf16 rows at key_row_stride / value_row_stride; slot_mapping: (batch,) int32, slots
  * outside [0, num_blocks*block_size) skipped; every other argument as nva_decode (same workspace,
  * nva_decode_workspace_bytes).  It has no single counterpart in the reference.
- * When nva_decode's plan is the small-batch spread mode, or the balanced mode over a bf16 cache,
- * the store runs inside the decode launch: the wave that reads key cache_seqlens[b]-1 writes the
- * new rows and uses them from registers.
- * That equals store-then-decode when slot_mapping[b] is the slot of key cache_seqlens[b]-1 of
- * sequence b (as every decode step the reference runs has it: prepare_decode, model_runner.py
- * :218-229) and no other sequence of the batch reads that slot; otherwise the attention over the
- * new token's slot is unspecified (the store itself is done).  Other plans (fixed splits, an fp8
- * cache in balanced mode) run the store kernel, then the decode.  The fused paths need fewer than
- * 2^31 slots in the pool (num_blocks * block_size); larger pools store first.
+ * When nva_decode's plan is the small-batch spread mode (with more than one share per
+ * sequence), or the balanced mode over a bf16 cache, the store runs inside the decode call
+ * with no extra launch: for a sequence with keys, the wave that reads key cache_seqlens[b]-1
+ * writes the new rows and uses them from registers; the rows of a sequence with none
+ * (cache_seqlens[b] == 0, e.g. a padded graph row) are written by the merge kernel, after
+ * every read of the call.  The result is deterministic for any input and equals
+ * store-then-decode when (a) slot_mapping[b] is the slot of key cache_seqlens[b]-1 for every
+ * sequence with keys, as every decode step the reference runs has it (prepare_decode,
+ * model_runner.py:218-229), and (b) no sequence reads the slot of a row with no keys.  The
+ * reference's graph replay breaks (b): run_model zero-fills slot_mapping
+ * (model_runner.py:271-273), so padded rows write slot 0, which a live sequence may own; here
+ * that sequence reads slot 0's previous contents, the two calls would show it the padded row.
+ * A runner that pads with slot -1 meets (b).  A sequence with keys whose slot breaks (a)
+ * leaves the attention over that slot unspecified (the store itself is done).  Other plans
+ * (fixed splits, an fp8 cache in balanced mode, one spread share) run the store kernel, then
+ * the decode: exactly the two calls.  The fused paths need fewer than 2^31 slots in the pool
+ * (num_blocks * block_size); larger pools store first.
  */
 int nva_store_decode(const void* key, int64_t key_row_stride,
                      const void* value, int64_t value_row_stride,

@@ -206,12 +206,29 @@ int nva_prefill(const void* q, int64_t q_row_stride, const void* k, int64_t k_ro
   if (workspace) {
     p.split_ctl = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + nva::kPrefillSplitCtlOffset);
     p.split_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + nva::kPrefillSplitPartOffset);
+    p.split_err = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + nva::kPrefillErrOffset);
   }
   return hip_status(nva::launch_prefill(p, max_seqlen_q, max_seqlen_k, static_cast<hipStream_t>(stream)),
                     "prefill launch");
 }
 
 int64_t nva_prefill_workspace_bytes(void) { return nva::kPrefillWorkspaceBytes; }
+
+int nva_prefill_workspace_errors(void* workspace, int64_t workspace_bytes, uint32_t* errors, void* stream) {
+  if (!workspace || !errors) return fail(NVA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (workspace_bytes < nva::kPrefillWorkspaceBytes || !aligned(workspace, 256))
+    return fail(NVA_ERR_INVALID_ARGUMENT, "prefill workspace must be 256-byte aligned and hold %lld bytes",
+                static_cast<long long>(nva::kPrefillWorkspaceBytes));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  void* word = static_cast<char*>(workspace) + nva::kPrefillErrOffset;
+  uint32_t host = 0;
+  hipError_t e = hipMemcpyAsync(&host, word, sizeof(host), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipMemsetAsync(word, 0, sizeof(uint32_t), s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_status(e, "prefill workspace error word");
+  *errors = host;
+  return ok();
+}
 
 int64_t nva_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                    int32_t max_blocks_per_seq, int32_t block_size, int32_t kv_dtype,
@@ -366,14 +383,17 @@ int decode_impl(const void* q, int64_t q_row_stride, const void* k_cache, const 
   p.spread = plan.spread;
   p.head_dim = head_dim;
   p.scale_log2 = softmax_scale * kLog2e;
+  p.kv_fp8 = kv_dtype == NVA_DTYPE_FP8_E4M3 ? 1 : 0;
   if (store) {
-    // The spread mode, and the balanced mode over a bf16 cache, store inside
-    // their own launch (16-byte source pieces); otherwise the store kernel
-    // runs first.
+    // The spread mode with more than one share, and the balanced mode over a
+    // bf16 cache, store inside their own launch (16-byte source pieces): the
+    // rows of sequences with keys in the decode kernel, those of sequences
+    // with none in the merge kernel that follows it.  Otherwise the store
+    // kernel runs first.
     // (The fused kernels compare slots in 32 bits: pools below 2^31 slots.)
     const bool bf16_vec = kv_dtype == NVA_DTYPE_BF16 && store_vec == 16;
     const bool small_pool = num_blocks * block_size < (int64_t{1} << 31);
-    if (small_pool && ((plan.spread > 0 && (kv_dtype == NVA_DTYPE_FP8_E4M3 || store_vec == 16)) ||
+    if (small_pool && ((plan.spread > 1 && (kv_dtype == NVA_DTYPE_FP8_E4M3 || store_vec == 16)) ||
                        (plan.balanced_ranges > 0 && bf16_vec))) {
       p.new_k = static_cast<const uint16_t*>(store->key);
       p.new_v = static_cast<const uint16_t*>(store->value);

@@ -51,14 +51,17 @@ struct DecodeParams {
   int32_t balanced_ranges;    // balanced mode: number of step ranges P (0 = fixed mode)
   int32_t spread;             // > 0: spread mode with that many shares per sequence (small batches)
   int32_t head_dim;           // 64 or 128
-  // Store fused into the spread launch (null new_k: none): row b of new_k /
-  // new_v (bf16, nkv * d elements) goes to cache slot slot_mapping[b].
+  // Store fused into the decode launch (null new_k: none): row b of new_k /
+  // new_v (bf16, nkv * d elements) goes to cache slot slot_mapping[b].  Rows
+  // of sequences with keys are stored by the wave that reads key ctx-1; rows
+  // of sequences with none are stored by the merge kernel, after every read.
   const uint16_t* new_k;
   const uint16_t* new_v;
   int64_t new_k_stride;
   int64_t new_v_stride;
   const int32_t* slot_mapping;
   float scale_log2;           // softmax_scale * log2(e)
+  int32_t kv_fp8;             // 1: e4m3fn cache (k_scale / v_scale), 0: bf16
 };
 
 struct PrefillParams {
@@ -88,14 +91,18 @@ struct PrefillParams {
   uint32_t* queue;            // null: static item order; else kPrefillQueueWords zeroed words
   // Key halving of the direct grid: items of at least split_tiles
   // key tiles (0: off) run as two workgroups over the two halves of their key
-  // tiles, merged by the one that finishes second.  At most split_slots such
-  // items; each has two zeroed control words in split_ctl and
+  // tiles, merged by the second to arrive.  At most split_slots such items;
+  // each has kPrefillSplitCtlWords control words in split_ctl and
   // kPrefillSplitPartFloats floats of partial results in split_part.
   int32_t split_tiles;
   int32_t split_slots;
   int32_t split_cus;          // compute units: with the real items, they cap the split items
   uint32_t* split_ctl;
   float* split_part;
+  // split_err[0]: error bits (kPrefillErrSplitWait), set by the kernel, cleared
+  // only by the host; split_err[1]: the merge wait's poll limit (0: the
+  // default bound, n > 0: n - 1 polls), written by the host.
+  uint32_t* split_err;
 };
 
 struct QKNormRopeParams {
@@ -146,16 +153,29 @@ constexpr int kPrefillMaxGroup = 256;        // rows per prefill workgroup bound
 // then the count of finished workgroups.  Zero on entry, zero again on exit.
 constexpr int kPrefillQueueLanes = 8;
 constexpr int kPrefillQueueWords = kPrefillQueueLanes + 1;
-// Key-halved items of the direct grid: the control words (a finish count and a
-// ready flag per slot, zero on entry and on exit) at byte kPrefillSplitCtlOffset,
+// Key-halved items of the direct grid: three control words per slot at byte
+// kPrefillSplitCtlOffset -- an arrival count (two per use: the even arrival
+// publishes its partial, the odd one merges), a ready word (the slot's epoch
+// + 1 once the partial is published) and the slot's epoch (uses completed) --
 // then one partial per slot from kPrefillSplitPartOffset: O (256 rows x up to
-// 128 head dims, float32, unnormalised) and each row's maximum and sum.
+// 128 head dims, float32, unnormalised) and each row's maximum and sum.  A
+// zeroed workspace is a valid start; every call leaves the words consistent
+// (arrival count = 2 x epoch, ready word <= epoch), so a ready word left by
+// an earlier call never matches a later one.
 constexpr int kPrefillSplitSlots = 64;
+constexpr int kPrefillSplitCtlWords = 3;
 constexpr int64_t kPrefillSplitPartFloats = 256 * 128 + 2 * 512;
+constexpr int64_t kPrefillErrOffset = 128;  // error word, then the poll-limit word
 constexpr int64_t kPrefillSplitCtlOffset = 256;
 constexpr int64_t kPrefillSplitPartOffset = 1024;
 constexpr int64_t kPrefillWorkspaceBytes = kPrefillSplitPartOffset + kPrefillSplitSlots * kPrefillSplitPartFloats * 4;
-static_assert(kPrefillSplitCtlOffset + 8 * kPrefillSplitSlots <= kPrefillSplitPartOffset, "control words fit");
+static_assert(kPrefillSplitCtlOffset + 4 * kPrefillSplitCtlWords * kPrefillSplitSlots <= kPrefillSplitPartOffset,
+              "control words fit");
+static_assert(kPrefillQueueWords * 4 <= kPrefillErrOffset && kPrefillErrOffset + 8 <= kPrefillSplitCtlOffset,
+              "error words fit between the queue and the control words");
+// Error bit: a key-half merge gave up waiting for its partial (the item's rows
+// were written as NaN).
+constexpr uint32_t kPrefillErrSplitWait = 1u;
 // Static device scratch of nva_decode_noalloc (bytes, per GPU).
 constexpr int64_t kDecodeScratchBytes = int64_t{32} << 20;
 static_assert(kPrefillQueueWords * 4 <= kPrefillSplitCtlOffset, "queue fits the workspace");

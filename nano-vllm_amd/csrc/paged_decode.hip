@@ -677,13 +677,14 @@ __global__ __launch_bounds__(64) void paged_decode_spread_kernel(DecodeParams p)
   const int n = lane & 15;
   const int g = lane >> 4;
   if constexpr (STORE) {
-    // The share holding key ctx-1 (share 0 of an empty sequence) stores the
-    // new token's rows of this kv head.  When slot_mapping[b] is key ctx-1's
-    // slot -- what every decode step produces -- that share's own read of the
-    // key is patched from registers, so no other share reads the slot and
-    // the result equals store-then-decode without waiting for the store.
+    // The share holding key ctx-1 stores the new token's rows of this kv
+    // head.  When slot_mapping[b] is key ctx-1's slot -- what every decode
+    // step produces -- that share's own read of the key is patched from
+    // registers, so no other share reads the slot and the result equals
+    // store-then-decode without waiting for the store.  An empty sequence's
+    // rows are stored by the merge kernel, after every read of this launch.
     const int64_t slot = __builtin_amdgcn_readfirstlane(p.slot_mapping[b]);
-    const int holder = ctx > 0 ? (ctx - 1) / (32 * per) : 0;
+    const int holder = ctx > 0 ? (ctx - 1) / (32 * per) : -1;
     NewRow<FP8, D> nr;
     const bool stores = r == holder && slot >= 0 && slot < static_cast<int64_t>(p.num_blocks) * p.block_size;
     // lanes 0..D/8-1 store the key row, lanes 32.. the value row, 8 elements
@@ -697,11 +698,9 @@ __global__ __launch_bounds__(64) void paged_decode_spread_kernel(DecodeParams p)
       const uint16_t* vin = p.new_v + b * p.new_v_stride + kvh * D;
       nr.load(kin, vin, n, g, FP8 ? p.k_scale[kvh] : 1.f, FP8 ? p.v_scale[kvh] : 1.f);
       x = ld16((is_v ? vin : kin) + 8 * (j & (D / 8 - 1)));  // every lane loads (no branch), D/8 of them store
-      if (ctx > 0) {
-        nr.step = ((ctx - 1) >> 5) - (k_begin >> 5);
-        nr.row = (ctx - 1) & 31;
-        nr.slot = static_cast<int>(slot);
-      }
+      nr.step = ((ctx - 1) >> 5) - (k_begin >> 5);
+      nr.row = (ctx - 1) & 31;
+      nr.slot = static_cast<int>(slot);
     }
     if (stores)
       segment_accumulate<FP8, true, D, true, true>(p, kvh, b, k_begin, k_end, acc, m_run, l, bt_row, nr);
@@ -806,28 +805,6 @@ __device__ __forceinline__ int64_t used_ranges(int64_t P, int64_t T) {
   return cap < 1 ? 1 : (P < cap ? P : cap);
 }
 
-// The new token's K and V rows of (b, kvh) written by one thread: a sequence
-// with no context has no step, so no segment holder stores them.
-template <bool FP8, int D>
-__device__ void store_new_rows_thread(const DecodeParams& p, int b, int kvh, int64_t slot) {
-  constexpr int EB = FP8 ? 1 : 2;
-#pragma unroll 1
-  for (int which = 0; which < 2; ++which) {
-    const uint16_t* src = (which ? p.new_v + b * p.new_v_stride : p.new_k + b * p.new_k_stride) + kvh * D;
-    char* dst = static_cast<char*>(const_cast<void*>(which ? p.v_cache : p.k_cache)) +
-                (slot * p.num_kv_heads + kvh) * D * EB;
-    const float sc = FP8 ? (which ? p.v_scale[kvh] : p.k_scale[kvh]) : 1.f;
-#pragma unroll 1
-    for (int j = 0; j < D / 8; ++j) {
-      const u32x4 x = ld16(src + 8 * j);
-      if constexpr (FP8)
-        *reinterpret_cast<u32x2*>(dst + 8 * j) = bf16x8_to_e4m3fn(x, sc);
-      else
-        *reinterpret_cast<u32x4*>(dst + 16 * j) = x;
-    }
-  }
-}
-
 template <bool FP8, int WAVES, bool PREFETCH, int D, bool STORE = false>
 __global__ __launch_bounds__(64 * WAVES) void paged_decode_balanced_kernel(DecodeParams p) {
   constexpr int CH = 64 * WAVES;  // sequences per scan chunk
@@ -852,17 +829,6 @@ __global__ __launch_bounds__(64 * WAVES) void paged_decode_balanced_kernel(Decod
     const int incl = block_scan_incl<WAVES>(st, s_wsum, tot);
     if (write_prefix && b < B) p.ws_prefix[b] = T + incl - st;
     T += tot;
-    if constexpr (STORE) {
-      // range 0 of each kv-head group stores the rows of sequences with no context
-      if (blockIdx.x == 0 && b < B && st == 0) {
-        const int64_t slot = p.slot_mapping[b];
-        if (slot >= 0 && slot < static_cast<int64_t>(p.num_blocks) * p.block_size)
-#pragma unroll 1
-          for (int w = 0; w < WAVES; ++w)
-            if (static_cast<int>(blockIdx.y) * WAVES + w < p.num_kv_heads)
-              store_new_rows_thread<FP8, D>(p, b, static_cast<int>(blockIdx.y) * WAVES + w, slot);
-      }
-    }
   }
   if (write_prefix && tid == 0) p.ws_prefix[B] = T;
   const int64_t P = used_ranges(p.balanced_ranges, T);
@@ -921,6 +887,27 @@ __global__ __launch_bounds__(64 * WAVES) void paged_decode_balanced_kernel(Decod
 constexpr int kMergeHeads = 4;    // heads (waves) per merge workgroup
 constexpr int kMergeWideMin = 8;  // ranges per sequence (on average) from which the merge is WIDE
 
+// The new token's K and V rows of (b, kvh) for a sequence with no keys, when
+// the store is fused into the decode launch: no decode wave reads key ctx-1 of
+// such a sequence, so the merge kernel -- stream-ordered after every read of
+// the decode launch -- stores them.  One wave: lanes 0..d/8-1 write the key
+// row, lanes 32..32+d/8-1 the value row, 8 elements each (fp8: quantised as
+// the store kernel does).  Slots outside the pool are skipped.
+__device__ void store_empty_rows_wave(const DecodeParams& p, int b, int kvh, int lane) {
+  const int64_t slot = p.slot_mapping[b];
+  const int j = lane & 31;
+  if (slot < 0 || slot >= p.num_blocks * p.block_size || 8 * j >= p.head_dim) return;
+  const bool is_v = lane >= 32;
+  const u32x4 x = ld16((is_v ? p.new_v + b * p.new_v_stride : p.new_k + b * p.new_k_stride) +
+                       static_cast<int64_t>(kvh) * p.head_dim + 8 * j);
+  const int64_t elem = (slot * p.num_kv_heads + kvh) * p.head_dim + 8 * j;
+  char* base = static_cast<char*>(const_cast<void*>(is_v ? p.v_cache : p.k_cache));
+  if (p.kv_fp8)
+    *reinterpret_cast<u32x2*>(base + elem) = bf16x8_to_e4m3fn(x, is_v ? p.v_scale[kvh] : p.k_scale[kvh]);
+  else
+    *reinterpret_cast<u32x4*>(base + 2 * elem) = x;
+}
+
 template <bool WIDE>
 __global__ __launch_bounds__(64 * kMergeHeads) void decode_merge_kernel(DecodeParams p) {
   const int hgroups = (p.num_heads + kMergeHeads - 1) / kMergeHeads;
@@ -950,6 +937,7 @@ __global__ __launch_bounds__(64 * kMergeHeads) void decode_merge_kernel(DecodePa
     zero = count == 0;
   }
   if (h >= p.num_heads) return;
+  if (zero && p.new_k && h % p.group == 0 && (!WIDE || wq == 0)) store_empty_rows_wave(p, b, h / p.group, lane);
   // A partial slot holds data unless it is a balanced range with no steps (P > T).
   const int64_t T = p.balanced_ranges > 0 ? p.ws_prefix[p.batch] : 0;
   const int64_t PU = p.balanced_ranges > 0 ? used_ranges(p.balanced_ranges, T) : 0;
@@ -1050,6 +1038,7 @@ __global__ __launch_bounds__(64) void decode_spread_merge_kernel(DecodeParams p)
   load_batch(0);
   int per, shares;
   spread_shares((clamped_len(p, b) + 31) >> 5, p.spread, per, shares);
+  if (shares == 0 && p.new_k && h % p.group == 0) store_empty_rows_wave(p, b, h / p.group, lane);
   if (shares <= 1) return;  // written directly by the decode kernel
   float M = kNegInf, L = 0.f, o0 = 0.f, o1 = 0.f;
   for (int s0 = 0;;) {

@@ -375,33 +375,46 @@ __device__ __forceinline__ void key_half(const PrefillParams& p, ItemDesc& d, in
   d.split_slot = slot;
 }
 
-// Bound on the merging workgroup's wait for the other half's partial.  That
-// half has already counted itself finished, so only its stores remain and the
-// wait ends within microseconds; the bound only keeps a wave from spinning
-// for ever should that ever fail.
-constexpr int kSplitSpinMax = 1 << 20;
+// Bound on the merging workgroup's wait for the other half's partial.  With
+// the control words consistent, that half arrived first and only its stores
+// remain, so the wait ends within microseconds (and with the arrival count out
+// of step the other half is already running or next in line); the bound keeps
+// a wave from spinning for ever should that ever fail.  Each poll sleeps ~128
+// cycles after a device-scope load: about 30 ms in all.
+constexpr uint32_t kSplitSpinMax = 1u << 16;
 
-// End of one key half of a split item, after the loop: the workgroup that
-// finishes first writes its unnormalised O, row maxima and row sums to the
-// item's slot and returns false; the second waits for them, folds them into
-// its own acc and l (both rescaled to the larger maximum) and returns true.
-// It also zeroes the slot's control words for the next call.
+// End of one key half of a split item, after the loop.  Thread 0 counts the
+// arrival and reads the slot's epoch E and the poll limit in one round trip.
+// The even arrival writes its unnormalised O, row maxima and row sums to the
+// item's slot, publishes them with the ready word E + 1 and returns false.
+// The odd arrival waits for that ready word, folds the partial into its own
+// acc and l (both rescaled to the larger maximum), advances the slot to epoch
+// E + 1 (arrival count 2E + 2) and returns true.  A ready word from an earlier
+// epoch never equals E + 1, so nothing published by an earlier call (or late,
+// after a wait gave up) is taken for this call's partial.  If the wait gives
+// up, the item's rows become NaN, the error bit is set in split_err[0] and the
+// slot advances all the same.
 template <int D>
 __device__ __forceinline__ bool merge_key_halves(const PrefillParams& p, char* smem_all, int slot,
                                                  f32x16 (&acc)[D / 32], float m_run, float& l) {
   constexpr int NJD = D / 32;
   constexpr int kThreads = 64 * kWaves;
-  uint32_t* ctl = p.split_ctl + 2 * slot;
+  uint32_t* ctl = p.split_ctl + kPrefillSplitCtlWords * slot;
   float* part = p.split_part + static_cast<int64_t>(slot) * kPrefillSplitPartFloats;
   float4* pacc = reinterpret_cast<float4*>(part);
   float* pm = part + kRows * 128;
   const int tid = threadIdx.x;
-  int* s_role = reinterpret_cast<int*>(smem_all);
+  uint32_t* s_ctl = reinterpret_cast<uint32_t*>(smem_all);
   barrier_lds();  // every wave is done with the ring
-  if (tid == 0) *s_role = static_cast<int>(atomicAdd(ctl, 1u));
+  if (tid == 0) {
+    s_ctl[0] = atomicAdd(ctl, 1u);
+    s_ctl[1] = __hip_atomic_load(ctl + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_ctl[2] = __hip_atomic_load(p.split_err + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   barrier_lds();
-  const int role = __builtin_amdgcn_readfirstlane(*s_role);
-  if (role == 0) {
+  const uint32_t arrival = __builtin_amdgcn_readfirstlane(s_ctl[0]);
+  const uint32_t epoch = __builtin_amdgcn_readfirstlane(s_ctl[1]);
+  if ((arrival & 1u) == 0) {
 #pragma unroll
     for (int jd = 0; jd < NJD; ++jd)
 #pragma unroll
@@ -415,20 +428,42 @@ __device__ __forceinline__ bool merge_key_halves(const PrefillParams& p, char* s
     // of this XCD, so one per workgroup rather than one per wave.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     barrier_lds();
-    if (tid == 0) __hip_atomic_store(ctl + 1, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(ctl + 1, epoch + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     return false;
   }
   if (tid == 0) {
     // Poll with relaxed loads (an acquire per poll would invalidate this XCD's
     // L2 each time, under every other workgroup on it), then acquire once.
-    for (int k = 0; k < kSplitSpinMax &&
-                    __hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u; ++k)
+    const uint32_t lim = s_ctl[2];
+    const uint32_t polls = lim == 0u ? kSplitSpinMax : lim - 1u;
+    uint32_t got = 0u;
+    for (uint32_t k = 0; k < polls; ++k) {
+      if (__hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch + 1u) {
+        got = 1u;
+        break;
+      }
       __builtin_amdgcn_s_sleep(2);
+    }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    __hip_atomic_store(ctl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(ctl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!got) atomicOr(p.split_err, kPrefillErrSplitWait);
+    __hip_atomic_store(ctl, 2u * (epoch + 1u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ctl + 2, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_ctl[3] = got;
   }
   barrier_lds();
+  if (__builtin_amdgcn_readfirstlane(s_ctl[3]) == 0u) {
+    // The partial never came: the item's rows become NaN (bits laundered
+    // through an empty asm, so no arithmetic on them is folded).
+    uint32_t nan_bits = 0x7fc00000u;
+    asm volatile("" : "+v"(nan_bits));
+    const float qnan = __builtin_bit_cast(float, nan_bits);
+#pragma unroll
+    for (int jd = 0; jd < NJD; ++jd)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[jd][e] = qnan;
+    l = 1.f;
+    return true;
+  }
   // the other waves' loads of the partial come after thread 0's acquire (the
   // barrier orders them); a workgroup-scope acquire keeps them after it
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");

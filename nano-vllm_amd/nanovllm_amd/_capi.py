@@ -21,6 +21,10 @@ NVA_ERR_WORKSPACE = 4
 NVA_DTYPE_BF16 = 0
 NVA_DTYPE_FP8_E4M3 = 1
 
+NVA_PREFILL_ERR_SPLIT_WAIT = 1
+# byte offset of the prefill workspace's poll-limit word (a test hook: 0 = default bound)
+NVA_PREFILL_SPLIT_WAIT_LIMIT_OFFSET = 132
+
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -47,6 +51,9 @@ SIGNATURES = {
         _c_void_p, _i64, _c_void_p,        # workspace, workspace_bytes, stream
     ]),
     "nva_prefill_workspace_bytes": (_i64, []),
+    "nva_prefill_workspace_errors": (_i32, [
+        _c_void_p, _i64, ctypes.POINTER(ctypes.c_uint32), _c_void_p,  # workspace, bytes, errors, stream
+    ]),
     "nva_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "nva_store_decode": (_i32, [
         _c_void_p, _i64, _c_void_p, _i64,  # key, key_row_stride, value, value_row_stride

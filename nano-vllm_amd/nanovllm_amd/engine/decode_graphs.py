@@ -13,10 +13,14 @@ layer, Attention.forward(q, k, v) under the decode Context, i.e. store_kvcache o
 the new token then paged decode (attention.py:58-79).  q/k/v of the step are
 static inputs (in the model they come from the layer's projection).
 
-One deliberate difference (reference quirk Q1): the reference zero-fills the
-slot mapping, so padded rows write their K/V into slot 0, which belongs to a
-live sequence.  This harness pads the slot mapping with -1, which the store
-skips; padded rows see zero context length and produce zero rows.
+Padding of the slot mapping (reference quirk Q1).  The reference zero-fills it,
+so padded rows write their K/V into slot 0, which may belong to a live sequence.
+pad_slot=0 reproduces that exactly: each layer runs the reference's two calls
+(store, then decode), so a live sequence owning slot 0 reads the padded row as
+the reference's does.  The default pad_slot=-1 is skipped by the store: padded
+rows leave the cache alone and produce zero rows, and with no padded row writing
+a slot, each layer's store runs inside its decode launch (Attention's
+fuse_decode_store), one graph node fewer per layer.
 """
 from __future__ import annotations
 
@@ -65,8 +69,20 @@ class DecodeGraphs:
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.pool = None
 
+    def _call_layers(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> list[torch.Tensor]:
+        """Every layer's forward, fused store+decode only under -1 padding."""
+        outs = []
+        for layer in self.layers:
+            prev = layer.fuse_decode_store
+            layer.fuse_decode_store = self.pad_slot < 0
+            try:
+                outs.append(layer(q, k, v))
+            finally:
+                layer.fuse_decode_store = prev
+        return outs
+
     def _step(self, bs: int) -> list[torch.Tensor]:
-        return [layer(self.q[:bs], self.k[:bs], self.v[:bs]) for layer in self.layers]
+        return self._call_layers(self.q[:bs], self.k[:bs], self.v[:bs])
 
     @torch.inference_mode()
     def capture(self) -> "DecodeGraphs":
@@ -98,10 +114,10 @@ class DecodeGraphs:
         if size is None or block_tables.shape[1] > self.max_num_blocks:
             set_context(False, slot_mapping=slot_mapping, context_lens=context_lens, block_tables=block_tables)
             try:
-                return [layer(q, k, v) for layer in self.layers]
+                return self._call_layers(q, k, v)
             finally:
                 reset_context()
-        # static buffers: zero, live rows in (model_runner.py:271-280); the slot pad is -1
+        # static buffers: zero, live rows in (model_runner.py:271-280); slots padded with pad_slot
         self.q.zero_()
         self.k.zero_()
         self.v.zero_()

@@ -45,9 +45,26 @@ def _stream(t: torch.Tensor) -> int:
 
 # One prefill workspace per (device, stream) -- the work queue, and the
 # control words and partials of the key halves -- zeroed once: every completed
-# nva_prefill call leaves its control words zero again.  Calls on one stream
-# run one after another, so they can share it; different streams get their own.
+# nva_prefill call leaves its control words consistent for the next.  Calls on
+# one stream run one after another, so they can share it; different streams
+# get their own.
 _PREFILL_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def prefill_workspace_errors() -> dict[tuple[int, int], int]:
+    """Error bits each prefill workspace has collected since the last check, read
+    and cleared (nva_prefill_workspace_errors; waits for each workspace's stream).
+    Non-zero bits (NVA_PREFILL_ERR_SPLIT_WAIT) mean some prefill wrote NaN rows for
+    an item whose key-half merge gave up waiting.  {(device, stream): bits}."""
+    import ctypes
+    lib = _capi.load()
+    out = {}
+    for (dev, stream), ws in _PREFILL_WORKSPACES.items():
+        bits = ctypes.c_uint32(0)
+        with torch.cuda.device(dev):
+            _capi.check(lib.nva_prefill_workspace_errors(ws.data_ptr(), ws.numel(), ctypes.byref(bits), stream))
+        out[(dev, stream)] = int(bits.value)
+    return out
 
 
 def _prefill_workspace(device: torch.device, stream: int) -> torch.Tensor | None:
@@ -61,6 +78,29 @@ def _prefill_workspace(device: torch.device, stream: int) -> torch.Tensor | None
         ws = torch.zeros(int(_capi.load().nva_prefill_workspace_bytes()), dtype=torch.uint8, device=device)
         _PREFILL_WORKSPACES[key] = ws
     return ws
+
+
+# Packed bf16 rows of the fp8 prefix-cached prefill's gather, one buffer per
+# (device, stream), grown to the largest call seen and reused: calls on one stream
+# run one after another, and the prefill that reads the rows is ordered before the
+# next call's gather overwrites them.
+_GATHER_BUFFERS: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _gather_rows(device: torch.device, stream: int, rows: int, row_elems: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(k, v) views of rows x row_elems bf16 each.  Under graph capture a fresh
+    tensor is taken from the graph's pool instead (its lifetime is the graph's)."""
+    n = rows * row_elems
+    if torch.cuda.is_current_stream_capturing():
+        buf = torch.empty(2 * n, dtype=_BF16, device=device)
+    else:
+        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+        buf = _GATHER_BUFFERS.get(key)
+        if buf is None or buf.numel() < 2 * n:
+            _GATHER_BUFFERS.pop(key, None)
+            buf = torch.empty(2 * n, dtype=_BF16, device=device)
+            _GATHER_BUFFERS[key] = buf
+    return buf[:n], buf[n:2 * n]
 
 
 def _check_device(device: torch.device, **tensors) -> None:
@@ -184,9 +224,11 @@ def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ma
             # dequantise each sequence's pages into packed rows, then the packed prefill
             _check_device(q.device, k=k, v=v, cu_seqlens_k=cu_seqlens_k, block_table=block_table,
                           k_scale=k_scale, v_scale=v_scale)
+            # rows of every sequence's keys at cu_seqlens_k[s]: at most num_seqs *
+            # max_seqlen_k (the total itself lives on the device)
             rows = num_seqs * int(max_seqlen_k)
-            kp = torch.empty((rows, nkv, d), dtype=_BF16, device=q.device)
-            vp = torch.empty((rows, nkv, d), dtype=_BF16, device=q.device)
+            kf, vf = _gather_rows(q.device, _stream(q), rows, nkv * d)
+            kp, vp = kf.view(rows, nkv, d), vf.view(rows, nkv, d)
             _capi.check(_capi.load().nva_gather_kv(
                 k.data_ptr(), v.data_ptr(), code, _ptr(k_scale), _ptr(v_scale), num_blocks,
                 bt_ptr, bt_stride, max_blocks, block_size, cu_seqlens_k.data_ptr(), num_seqs, int(max_seqlen_k),
@@ -237,9 +279,13 @@ def store_and_decode(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, k_
     """The decode branch of Attention.forward as one call: store_kvcache of the new
     rows (attention.py:32-39), then flash_attn_with_kvcache (attention.py:75-77).
     The spread mode (small batches) and the balanced mode over a bf16 cache run the
-    store inside the decode launch (nva_store_decode); the result equals the two
-    calls when slot_mapping[b] is the slot of key cache_seqlens[b]-1, as
-    prepare_decode (model_runner.py:218-229) produces it."""
+    store inside the decode launch (nva_store_decode).  The result equals the two
+    calls when slot_mapping[b] is the slot of key cache_seqlens[b]-1 for every
+    sequence with keys, as prepare_decode (model_runner.py:218-229) produces it, and
+    no sequence reads the slot of a row whose cache_seqlens is 0 (graph padding: use
+    slot -1).  Such rows are stored after every read of the call, so a sequence that
+    does read that slot sees its previous contents (the two calls would show it the
+    padded row)."""
     N = key.shape[0]
     if N != q.shape[0]:
         raise RuntimeError("one new key/value row per sequence")
@@ -293,7 +339,15 @@ def _decode_args(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale,
 
 
 class Attention(nn.Module):
-    """Drop-in for nanovllm.layers.attention.Attention (attention.py:42-79)."""
+    """Drop-in for nanovllm.layers.attention.Attention (attention.py:42-79).
+
+    fuse_decode_store (not in the reference, default False): when True the decode
+    branch runs the store and the attention as one call (store_and_decode), one
+    launch fewer per layer.  It equals the reference's store-then-decode only if no
+    padded row (context length 0) carries a slot that a live sequence reads; the
+    reference's run_model zero-fills slot_mapping (model_runner.py:271-273), so its
+    padded rows write slot 0 of block 0, which a live sequence may own.  Set it only
+    under a runner that pads slot_mapping with -1 (DecodeGraphs with pad_slot=-1)."""
 
     def __init__(self, num_heads, head_dim, scale, num_kv_heads):
         super().__init__()
@@ -304,6 +358,7 @@ class Attention(nn.Module):
         self.k_cache = self.v_cache = torch.tensor([])
         # fp8 cache extension: per-kv-head float32 scales, None for a bf16 cache
         self.k_scale = self.v_scale = None
+        self.fuse_decode_store = False
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
         q = q.view(-1, self.num_heads, self.head_dim)
@@ -312,7 +367,7 @@ class Attention(nn.Module):
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
         bound = k_cache.numel() and v_cache.numel()
-        if not context.is_prefill and bound:  # decode: store and attention as one call
+        if not context.is_prefill and bound and self.fuse_decode_store:  # store and attention as one call
             o = store_and_decode(q.unsqueeze(1), k, v, k_cache, v_cache, context.slot_mapping,
                                  context.context_lens, context.block_tables, softmax_scale=self.scale,
                                  k_scale=self.k_scale, v_scale=self.v_scale)

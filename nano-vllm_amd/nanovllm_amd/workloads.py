@@ -321,6 +321,25 @@ def config5(bulk_device="cpu", seed=SEEDS[5]) -> DecodeCase:
 CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
 
 
+# One GPU's share of a tensor-parallel group of 8 (qwen3.py:33-43 divides the query
+# and kv heads by the TP size, model_runner.py:117 sizes each rank's cache for its
+# nkv / tp heads): the same draws of lengths, pages and values as configs 4 and 5,
+# over one kv head.
+
+def config4_tp8(bulk_device="cpu", seed=SEEDS[4]) -> PrefillCase:
+    """Config 4 at Qwen3-8B's TP8 share: heads 4/1 (GQA 4), prefix 1024, suffix U[256,768]."""
+    gen = torch.Generator().manual_seed(seed)
+    lens = torch.randint(256, 769, (16,), generator=gen).tolist()
+    return make_prefill_case(lens, 4, 1, 64, prefix_len=1024, seed=seed, bulk_device=bulk_device,
+                             name="cfg4-tp8", gen=gen)
+
+
+def config5_tp8(bulk_device="cpu", seed=SEEDS[5]) -> DecodeCase:
+    """Config 5 at Qwen3-32B's TP8 share: heads 8/1 (GQA 8), fp8 cache, B=64, ctx U[16k,32k]."""
+    return make_decode_case(64, 8, 1, 16384, 32768, 8192, fp8=True, seed=seed, bulk_device=bulk_device,
+                            name="cfg5-tp8")
+
+
 @dataclass
 class ProducerCase:
     """Inputs of the fused qk-RMSNorm + rotary step (qwen3.py:91-105): q and k are

@@ -30,6 +30,14 @@ def store_kvcache(key, value, k_cache, v_cache, slot_mapping):
     v_cache.view(-1, D).index_copy_(0, idx, value.reshape(T, D))
 
 
+def store_kvcache_fp8(key, value, k_cache, v_cache, slot_mapping, k_scale, v_scale):
+    """The fp8 cache's store: e4m3fn(x / scale[h]) by torch's float8_e4m3fn cast, then
+    the byte rows copied as store_kvcache does (caches: float8_e4m3fn tensors)."""
+    k8 = (key.float() / k_scale.view(1, -1, 1)).to(torch.float8_e4m3fn).view(torch.uint8)
+    v8 = (value.float() / v_scale.view(1, -1, 1)).to(torch.float8_e4m3fn).view(torch.uint8)
+    store_kvcache(k8, v8, k_cache.view(torch.uint8), v_cache.view(torch.uint8), slot_mapping)
+
+
 def _gather(cache, table_row, L, bs):
     pages = table_row[: math.ceil(L / bs)].long()
     return cache.index_select(0, pages).reshape(-1, cache.shape[2], cache.shape[3])[:L]

@@ -118,6 +118,18 @@ def test_prefill_workspace_bytes(lib):
     assert n >= 4 * 9 and n % 256 == 0
 
 
+def test_prefill_workspace_errors_rejects(lib):
+    """Bad workspaces are refused before any HIP call (no GPU here)."""
+    import ctypes
+    bits = ctypes.c_uint32(7)
+    n = lib.nva_prefill_workspace_bytes()
+    assert lib.nva_prefill_workspace_errors(None, n, ctypes.byref(bits), None) == _capi.NVA_ERR_INVALID_ARGUMENT
+    assert lib.nva_prefill_workspace_errors(A, n, None, None) == _capi.NVA_ERR_INVALID_ARGUMENT
+    assert lib.nva_prefill_workspace_errors(A, n - 256, ctypes.byref(bits), None) == _capi.NVA_ERR_INVALID_ARGUMENT
+    assert lib.nva_prefill_workspace_errors(A + 64, n, ctypes.byref(bits), None) == _capi.NVA_ERR_INVALID_ARGUMENT
+    assert bits.value == 7
+
+
 def decode(lib, **kw):
     args = dict(q=A, q_row_stride=2048, k_cache=B, v_cache=C, kv_dtype=0, k_scale=None, v_scale=None,
                 num_blocks=2048, seqlens=A + 0x9000, block_table=A + 0xA000, bt_row_stride=8, max_blocks=8,

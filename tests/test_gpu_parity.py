@@ -519,7 +519,7 @@ def test_prefill_key_halves_paged(dev, monkeypatch, lens, prefix, nh, nkv, d, bs
     """Prefix-cached (paged) direct-grid launches with key halving: a split
     item's halves meet at the page boundary nearest its middle, and the second
     half reads the block-table row from that page on.  Every row against the
-    oracle and against whole items (no workspace); the control words zero."""
+    oracle and against whole items (no workspace); the control words consistent."""
     from nanovllm_amd import workloads as W
     from nanovllm_amd.layers import attention as A
     gen = None
@@ -536,7 +536,7 @@ def test_prefill_key_halves_paged(dev, monkeypatch, lens, prefix, nh, nkv, d, bs
     print(f"paged key halves lens={lens} prefix={prefix} nh={nh} nkv={nkv} d={d} bs={bs}", flush=True)
     halved = _run_prefill(case)
     ws = A._PREFILL_WORKSPACES[(dev.index or 0, torch.cuda.current_stream(dev).cuda_stream)]
-    assert int(ws[:_WS_CTL_BYTES].count_nonzero()) == 0, "the split slots must be left zero"
+    _assert_ws_consistent(ws)
     ref = prefill_reference(case)
     assert_attn_close(halved, ref, what=f"paged key halves bs={bs}")
     monkeypatch.setattr(A, "_prefill_workspace", lambda device, stream: None)
@@ -784,20 +784,41 @@ def test_prefill_work_queue_matches_static_order(dev, monkeypatch):
         print(f"work queue vs static: {case.name if hasattr(case, 'name') else 'case'}", flush=True)
         queued = _run_prefill(case)
         ws = A._PREFILL_WORKSPACES[(dev.index or 0, torch.cuda.current_stream(dev).cuda_stream)]
-        assert int(ws[:_WS_CTL_BYTES].count_nonzero()) == 0, "the queue must be left zero"
+        _assert_ws_consistent(ws)
         monkeypatch.setattr(A, "_prefill_workspace", lambda device, stream: None)
         static = _run_prefill(case, store=False)
         monkeypatch.setattr(A, "_prefill_workspace", orig)
         assert np.array_equal(queued, static)
         again = _run_prefill(case, store=False)
         assert np.array_equal(again, queued)
-        assert int(ws[:_WS_CTL_BYTES].count_nonzero()) == 0
+        _assert_ws_consistent(ws)
 
 
-# The prefill workspace's control words (the work queue, then the key-halving
-# slots' finish counts and ready flags) fill its first 1024 bytes; the rest holds
-# the key halves' partial results and is overwritten by every split call.
+# The prefill workspace's control words fill its first 1024 bytes: the work queue
+# (9 words from byte 0), the error word and the merge wait's poll-limit word (bytes
+# 128 and 132), then three words per key-halving slot from byte 256 (arrival count,
+# ready word, epoch).  The rest holds the key halves' partial results and is
+# overwritten by every split call.
 _WS_CTL_BYTES = 1024
+_WS_ERR, _WS_LIMIT, _WS_SLOTS = 128, 132, 256
+
+
+def _ws_words(ws):
+    return ws[:_WS_CTL_BYTES].cpu().numpy().view(np.uint32)
+
+
+def _assert_ws_consistent(ws):
+    """What every completed call leaves: the queue, error and limit words zero, and
+    each slot's arrival count twice its epoch with the ready word at the epoch (the
+    value a partial of the last completed use carries; the next use waits for
+    epoch + 1)."""
+    w = _ws_words(ws)
+    assert not w[:_WS_SLOTS // 4].any(), "the queue, error and limit words must be left zero"
+    slots = w[_WS_SLOTS // 4:].reshape(-1, 3)
+    count, ready, epoch = slots[:, 0].astype(np.int64), slots[:, 1].astype(np.int64), slots[:, 2].astype(np.int64)
+    assert np.array_equal(count, 2 * epoch), "arrival counts out of step with the epochs"
+    assert np.array_equal(ready, epoch), "ready words out of step with the epochs"
+    return epoch
 
 
 @pytest.mark.parametrize("lens,nh,nkv,d", [
@@ -815,7 +836,7 @@ def test_prefill_key_halves(dev, monkeypatch, lens, nh, nkv, d):
     workspace.  Without a workspace every item runs whole on the plain grid.
     Both against the oracle on every row (the early rows of an item see no key of
     its second half), the halves within the bf16 bar of the whole items, the
-    control words zero after each call, and a second call reusing the slots."""
+    control words consistent after each call, and a second call reusing the slots."""
     from nanovllm_amd import workloads as W
     from nanovllm_amd.layers import attention as A
     pages = sum(-(-x // 256) for x in lens) + 4
@@ -826,16 +847,88 @@ def test_prefill_key_halves(dev, monkeypatch, lens, nh, nkv, d):
     print(f"key halves lens={lens} nh={nh} nkv={nkv} d={d}", flush=True)
     halved = _run_prefill(case)
     ws = A._PREFILL_WORKSPACES[(dev.index or 0, torch.cuda.current_stream(dev).cuda_stream)]
-    assert int(ws[:_WS_CTL_BYTES].count_nonzero()) == 0, "the split slots must be left zero"
+    _assert_ws_consistent(ws)
     ref = prefill_reference(case)
     assert_attn_close(halved, ref, what=f"key halves {lens}")
     again = _run_prefill(case, store=False)
-    assert int(ws[:_WS_CTL_BYTES].count_nonzero()) == 0
+    _assert_ws_consistent(ws)
     assert_attn_close(again, ref, what=f"key halves, second call {lens}")
     monkeypatch.setattr(A, "_prefill_workspace", lambda device, stream: None)
     whole = _run_prefill(case, store=False)
     assert_attn_close(whole, ref, what=f"whole items {lens}")
     assert float(np.abs(halved - whole).max()) < 2e-2
+
+
+def _cfg2_case(dev):
+    from nanovllm_amd import workloads as W
+    lens = [512, 540, 147, 296, 319, 300, 927, 255]  # config 2's lengths: key halving on the compact grid
+    return W.make_prefill_case(lens, 16, 8, sum(-(-x // 256) for x in lens) + 4, seed=2202, bulk_device=dev)
+
+
+def test_prefill_key_half_wait_gives_up_loudly(dev):
+    """The key-half merge's bounded wait, forced to give up from the host: the
+    workspace's poll-limit word set to allow no poll, so every split item's merging
+    half gives up.  The call completes (every kernel exits), the split items' rows
+    come back NaN -- whole (position, head) rows, never mixed with numbers -- while
+    every other row matches the oracle, and the error word reports it (read and
+    cleared by prefill_workspace_errors).  With the limit word back to 0 the next
+    call is clean: every row against the oracle, no error, the words consistent."""
+    from nanovllm_amd import _capi
+    from nanovllm_amd.layers import attention as A
+    case = _cfg2_case(dev)
+    ref = prefill_reference(case)
+    clean = _run_prefill(case)
+    key = (dev.index or 0, torch.cuda.current_stream(dev).cuda_stream)
+    ws = A._PREFILL_WORKSPACES[key]
+    assert A.prefill_workspace_errors()[key] == 0
+    epoch0 = _assert_ws_consistent(ws)
+    assert_attn_close(clean, ref, what="key halves before the forced give-up")
+    off = _capi.NVA_PREFILL_SPLIT_WAIT_LIMIT_OFFSET
+    ws[off:off + 4] = torch.tensor([1, 0, 0, 0], dtype=torch.uint8, device=dev)  # n - 1 = 0 polls
+    print("prefill with the merge wait limited to no poll", flush=True)
+    forced = _run_prefill(case, store=False)
+    ws[off:off + 4] = 0
+    assert A.prefill_workspace_errors()[key] == _capi.NVA_PREFILL_ERR_SPLIT_WAIT
+    assert A.prefill_workspace_errors()[key] == 0  # cleared by the read
+    nan = np.isnan(forced)
+    assert nan.any(), "no split item gave up"
+    rows_nan = nan.all(axis=-1)
+    assert np.array_equal(rows_nan, nan.any(axis=-1)), "NaN must fill whole rows"
+    ok = ~rows_nan
+    assert_attn_close(forced[ok], ref[ok], what="rows of items that were not split")
+    epoch1 = _assert_ws_consistent(ws)
+    assert (epoch1 >= epoch0).all() and (epoch1 > epoch0).any()
+    again = _run_prefill(case, store=False)
+    assert A.prefill_workspace_errors()[key] == 0
+    assert_attn_close(again, ref, what="key halves after the forced give-up")
+    # (which half merges depends on which finishes first: equal up to float32 rounding)
+    assert float(np.abs(again - clean).max()) <= 1e-2
+    _assert_ws_consistent(ws)
+
+
+def test_prefill_key_halves_arrival_count_out_of_step(dev):
+    """A slot whose arrival count is odd at the start of a call (words out of step:
+    the first half to arrive takes the merging role and waits for the second) still
+    merges the right partial, and the call leaves the slot consistent again."""
+    from nanovllm_amd.layers import attention as A
+    case = _cfg2_case(dev)
+    ref = prefill_reference(case)
+    clean = _run_prefill(case)
+    key = (dev.index or 0, torch.cuda.current_stream(dev).cuda_stream)
+    ws = A._PREFILL_WORKSPACES[key]
+    epoch = _assert_ws_consistent(ws)
+    used = np.nonzero(epoch)[0]
+    assert used.size, "no split slot was used"
+    for s in used[:4]:
+        b = _WS_SLOTS + 12 * int(s)
+        count = int(2 * epoch[s] + 1)
+        ws[b:b + 4] = torch.tensor(list(count.to_bytes(4, "little")), dtype=torch.uint8, device=dev)
+    print(f"prefill with slots {used[:4].tolist()} out of step", flush=True)
+    odd = _run_prefill(case, store=False)
+    assert A.prefill_workspace_errors()[key] == 0
+    assert float(np.abs(odd - clean).max()) <= 1e-2
+    _assert_ws_consistent(ws)
+    assert_attn_close(odd, ref, what="key halves with the arrival count out of step")
 
 
 @pytest.mark.parametrize("prefix", [0, 256])
