@@ -89,7 +89,7 @@ int nva_store_kvcache(const void* key, int64_t key_row_stride,
  * keys sees keys j <= i + (Lk - Lq).  A query row with no visible key yields zeros.
  * max_seqlen_q bounds the launch grid (host value, graph-capture safe).
  * head_dim 64 or 128; a paged cache needs block_size % 64 == 0 and bf16.
- * workspace: NULL, or nva_prefill_workspace_bytes() bytes (about 8.7 MB), 256-byte aligned,
+ * workspace: NULL, or nva_prefill_workspace_bytes() bytes (about 17.3 MB), 256-byte aligned,
  *   holding zeros before its first use.  With it, a prefill over many work items hands
  *   them out dynamically (a work queue per XCD), and a prefill over few items (at most two
  *   per CU; paged caches with blocks of at most 512 keys) runs its longest items as two

@@ -162,12 +162,15 @@ constexpr int kPrefillQueueWords = kPrefillQueueLanes + 1;
 // zeroed workspace is a valid start; every call leaves the words consistent
 // (arrival count = 2 x epoch, ready word <= epoch), so a ready word left by
 // an earlier call never matches a later one.
-constexpr int kPrefillSplitSlots = 64;
+// 128 slots: a one-kv-head launch (a tensor-parallel share) splits up to 128 items,
+// as many as its free CUs take (64 slots held config 4's TP8 share at 44.3 us, 128
+// bring it to 41.9 us).
+constexpr int kPrefillSplitSlots = 128;
 constexpr int kPrefillSplitCtlWords = 3;
 constexpr int64_t kPrefillSplitPartFloats = 256 * 128 + 2 * 512;
 constexpr int64_t kPrefillErrOffset = 128;  // error word, then the poll-limit word
 constexpr int64_t kPrefillSplitCtlOffset = 256;
-constexpr int64_t kPrefillSplitPartOffset = 1024;
+constexpr int64_t kPrefillSplitPartOffset = 2048;
 constexpr int64_t kPrefillWorkspaceBytes = kPrefillSplitPartOffset + kPrefillSplitSlots * kPrefillSplitPartFloats * 4;
 static_assert(kPrefillSplitCtlOffset + 4 * kPrefillSplitCtlWords * kPrefillSplitSlots <= kPrefillSplitPartOffset,
               "control words fit");

@@ -794,13 +794,13 @@ def test_prefill_work_queue_matches_static_order(dev, monkeypatch):
         _assert_ws_consistent(ws)
 
 
-# The prefill workspace's control words fill its first 1024 bytes: the work queue
+# The prefill workspace's control words fill its first 2048 bytes: the work queue
 # (9 words from byte 0), the error word and the merge wait's poll-limit word (bytes
-# 128 and 132), then three words per key-halving slot from byte 256 (arrival count,
-# ready word, epoch).  The rest holds the key halves' partial results and is
+# 128 and 132), then three words per key-split slot from byte 256 (arrival count,
+# ready word, epoch; 128 slots).  The rest holds the partial results and is
 # overwritten by every split call.
-_WS_CTL_BYTES = 1024
-_WS_ERR, _WS_LIMIT, _WS_SLOTS = 128, 132, 256
+_WS_CTL_BYTES = 2048
+_WS_ERR, _WS_LIMIT, _WS_SLOTS, _WS_NSLOTS = 128, 132, 256, 128
 
 
 def _ws_words(ws):
@@ -814,7 +814,9 @@ def _assert_ws_consistent(ws):
     epoch + 1)."""
     w = _ws_words(ws)
     assert not w[:_WS_SLOTS // 4].any(), "the queue, error and limit words must be left zero"
-    slots = w[_WS_SLOTS // 4:].reshape(-1, 3)
+    end = _WS_SLOTS // 4 + 3 * _WS_NSLOTS
+    assert not w[end:].any(), "the words past the last slot must stay zero"
+    slots = w[_WS_SLOTS // 4:end].reshape(-1, 3)
     count, ready, epoch = slots[:, 0].astype(np.int64), slots[:, 1].astype(np.int64), slots[:, 2].astype(np.int64)
     assert np.array_equal(count, 2 * epoch), "arrival counts out of step with the epochs"
     assert np.array_equal(ready, epoch), "ready words out of step with the epochs"
