@@ -149,10 +149,10 @@ __device__ __forceinline__ void load_step(StepRegs<FP8>& r, const WaveItem& w, i
     const char* rp = w.kbase + (row0 + w.krow0 + 4 * t) * w.slot_bytes;
     if constexpr (!FP8) {
 #pragma unroll
-      for (int s = 0; s < D / 32; ++s) r.k[t][s] = ld16(rp + qk_dim<false>(s, w.g) * 2);
+      for (int s = 0; s < D / 32; ++s) r.k[t][s] = ld16_nt(rp + qk_dim<false>(s, w.g) * 2);
     } else {
 #pragma unroll
-      for (int u = 0; u < D / 64; ++u) r.k[t][u] = ld16(rp + 64 * u + 16 * w.g);
+      for (int u = 0; u < D / 64; ++u) r.k[t][u] = ld16_nt(rp + 64 * u + 16 * w.g);
     }
   }
   const bool has_cols = D == 128 || w.n < D / 8;
@@ -160,9 +160,9 @@ __device__ __forceinline__ void load_step(StepRegs<FP8>& r, const WaveItem& w, i
   for (int i = 0; i < 8; ++i) {
     const char* rp = w.vbase + (row0 + 8 * w.g + i) * w.slot_bytes;
     if constexpr (!FP8)
-      r.v[i] = has_cols ? ld16(rp + 16 * w.n) : u32x4{0u, 0u, 0u, 0u};
+      r.v[i] = has_cols ? ld16_nt(rp + 16 * w.n) : u32x4{0u, 0u, 0u, 0u};
     else
-      r.v[i] = has_cols ? ld8(rp + 8 * w.n) : u32x2{0u, 0u};
+      r.v[i] = has_cols ? ld8_nt(rp + 8 * w.n) : u32x2{0u, 0u};
   }
 }
 
@@ -211,10 +211,11 @@ __device__ __forceinline__ void load_step_buf(StepRegs<FP8>& r, const WaveItem& 
     if constexpr (!FP8) {
 #pragma unroll
       for (int s = 0; s < D / 32; ++s)
-        r.k[t][s] = __builtin_amdgcn_raw_buffer_load_b128(rs.k, ro + qk_dim<false>(s, w.g) * 2, 0, 0);
+        r.k[t][s] = __builtin_amdgcn_raw_buffer_load_b128(rs.k, ro + qk_dim<false>(s, w.g) * 2, 0, kBufNonTemporal);
     } else {
 #pragma unroll
-      for (int u = 0; u < D / 64; ++u) r.k[t][u] = __builtin_amdgcn_raw_buffer_load_b128(rs.k, ro + 64 * u + 16 * w.g, 0, 0);
+      for (int u = 0; u < D / 64; ++u)
+        r.k[t][u] = __builtin_amdgcn_raw_buffer_load_b128(rs.k, ro + 64 * u + 16 * w.g, 0, kBufNonTemporal);
     }
   }
   const bool has_cols = D == 128 || w.n < D / 8;
@@ -223,9 +224,9 @@ __device__ __forceinline__ void load_step_buf(StepRegs<FP8>& r, const WaveItem& 
   for (int i = 0; i < 8; ++i) {
     const int off = (8 * w.g + i) * sb + col;
     if constexpr (!FP8)
-      r.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs.v, off, 0, 0);
+      r.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs.v, off, 0, kBufNonTemporal);
     else
-      r.v[i] = __builtin_amdgcn_raw_buffer_load_b64(rs.v, off, 0, 0);
+      r.v[i] = __builtin_amdgcn_raw_buffer_load_b64(rs.v, off, 0, kBufNonTemporal);
   }
 }
 
@@ -609,8 +610,10 @@ struct DecodeShape<false> {
 template <>
 struct DecodeShape<true> {
   static constexpr int kWaves = 8;
-  static constexpr bool kPrefetch = false;
-  static constexpr bool kBuf = false;  // the buffer pipeline measured +0.8% at config 5
+  // buffer-resource steps, two in flight: with non-temporal loads, config 5 516.5 -> 508.6 us and
+  // its TP8 share 84.6 -> 82.1 us (plain loads without prefetch had been 0.8% ahead before)
+  static constexpr bool kPrefetch = true;
+  static constexpr bool kBuf = true;
   static constexpr int kTargetWaves = 2048;
 };
 
