@@ -46,9 +46,12 @@ def hipcc() -> str:
 
 # Per-file extras.  The prefill kernel's softmax never relies on NaN
 # propagation (masked scores are -inf, not NaN), so max() can skip the
-# IEEE quieting of its operands.
+# IEEE quieting of its operands.  Its atomics are single-lane (the work-queue
+# claims, the key-half arrivals), so the compiler's atomic optimizer only adds
+# a wait for the result right after each one; without it the wait moves to the
+# result's first use, which lets the first claim overlap the table loads.
 FILE_FLAGS = {
-    "varlen_prefill.hip": ["-fno-honor-nans"],
+    "varlen_prefill.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
 }
 
 

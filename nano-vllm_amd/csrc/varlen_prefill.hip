@@ -980,6 +980,18 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(
   const int T = p.num_q_tiles;
   const int BP = p.positions_per_tile;
   const int nkv = p.num_kv_heads;
+  constexpr int L = kPrefillQueueLanes;
+  const int NW = static_cast<int>(gridDim.x);
+  const int g = static_cast<int>(blockIdx.x);
+  // QUEUE: the launch guarantees NW % 8 == 0, so lane x is the XCD
+  const int x = g % L;
+  uint32_t* const claim_ctr = QUEUE ? p.queue + x : nullptr;
+  // The first claim goes out before the table is built, so its round trip
+  // overlaps the cu_seqlens loads (config 4: 203.2 -> 201.9 us).  A workgroup
+  // with no first item claims only indices >= NW, past every real item, so
+  // nothing it claims is lost.
+  uint32_t claim = 0;
+  if (QUEUE && tid == 0) claim = atomicAdd(claim_ctr, 1u);
 
   // level table: cnt[t] = #{s : ntq_s > t}; items of level t (query tile t of
   // those sequences, all kv heads) start at s_start[t] = nkv * sum_{t' > t} cnt[t']
@@ -1034,8 +1046,6 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(
   }
   __syncthreads();
   const int total = s_start[T];
-  const int NW = static_cast<int>(gridDim.x);
-  const int g = static_cast<int>(blockIdx.x);
   // Table item `item` (every item below `total` is a real tile: its sequence
   // has more than t query tiles), or an invalid descriptor past the end.
   auto desc_of = [&](int item) {
@@ -1053,10 +1063,6 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(
     const int kvh = j - rank * nkv;
     return item_desc(p, s_cu[0], s_cu[1], find_seq(s_ntq, S, t, rank), kvh, t);
   };
-  // QUEUE: the launch guarantees NW % 8 == 0, so lane x is the XCD
-  constexpr int L = kPrefillQueueLanes;
-  const int x = g % L;
-  uint32_t* const claim_ctr = QUEUE ? p.queue + x : nullptr;
   auto finish = [&]() {
     if (QUEUE && tid == 0 &&
         atomicAdd(p.queue + kPrefillQueueLanes, 1u) == static_cast<uint32_t>(NW - 1)) {
@@ -1068,8 +1074,6 @@ __global__ __launch_bounds__(64 * kWaves) void varlen_prefill_persistent_kernel(
     finish();
     return;
   }
-  uint32_t claim = 0;
-  if (QUEUE && tid == 0) claim = atomicAdd(claim_ctr, 1u);
   bf16x8 qop[D / 16];
   item_fetch_q<D>(p, cur, qop);
   item_fetch_tiles<PAGED, D>(p, smem_all, cur);
